@@ -1,0 +1,111 @@
+/*
+ * trianglemix.h -- C ABI of the MI355X (gfx950) TriangleMix paged sparse
+ * prefill attention library (libtrianglemix.so).
+ *
+ * Geometry is fixed to the reference operator's compiled ABI
+ * (operator/schema/triangle_paged_sparse_attention.json:38-89,
+ * operator/op_host/triangle_paged_sparse_attention.cpp:26-37):
+ *   query        [query_tokens, 32, 128]        bf16, contiguous
+ *   key_cache    [num_pages, 128, 8, 128]       bf16, contiguous (BSND pages)
+ *   value_cache  [num_pages, 128, 8, 128]       bf16, contiguous
+ *   block_table  [1, block_table_cols]          int32, logical page -> physical page
+ *   out          [query_tokens, 32, 128]        bf16, contiguous, written in place
+ * GQA 4:1 (query head h reads KV head h/4), page 128, sink 8, local window
+ * 512, dense tail 128, q_tile 32.
+ *
+ * All pointers are device pointers; `stream` is a hipStream_t (NULL = the
+ * null stream).  Every call is asynchronous: it validates its arguments on
+ * the host, enqueues exactly one kernel on `stream` and returns.  No call
+ * allocates device memory, synchronises, or reads device memory on the host.
+ * Arguments are validated before any HIP call, so a rejected call touches
+ * no device state.
+ */
+#ifndef TRIANGLEMIX_H
+#define TRIANGLEMIX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TM_ABI_VERSION 1
+
+/* Status codes. */
+#define TM_OK 0
+#define TM_ERR_INVALID_ARGUMENT 1 /* shape / attribute / pointer contract breach */
+#define TM_ERR_UNSUPPORTED 2      /* outside the fixed compiled geometry or limits */
+#define TM_ERR_WORKSPACE 3        /* workspace too small for this call */
+#define TM_ERR_LAUNCH 4           /* the HIP launch itself failed */
+
+/* ABI version of the loaded library (TM_ABI_VERSION it was built with). */
+int tm_abi_version(void);
+
+/* Static name of a status code. */
+const char* tm_status_string(int status);
+
+/* Human-readable detail of the last failing call on the calling thread
+ * (empty string if none).  The text mirrors the reference's TORCH_CHECK /
+ * tiling messages. */
+const char* tm_last_error(void);
+
+/*
+ * TriangleMix sparse prefill over one scheduler chunk: rows
+ * [query_start, seq_len) of a prompt of final length prompt_len.
+ * Rows q with 521 <= q < prompt_len-128 attend keys [0,8) U [q-512, q];
+ * all other rows attend [0, q].  One softmax per row over all its keys;
+ * fp32 accumulation; bf16 output rounded to nearest even.
+ *
+ * Replaces trianglemix::triangle_paged_sparse_attention.out
+ * (operator/torch_adapter/triangle_paged_attention_torch.cpp:140-178, schema
+ * :290-297) and the aclnnTrianglePagedSparseAttention launch it wraps
+ * (:161-176); validation follows check_inputs/check_output (:29-97) and
+ * TilingFunc (operator/op_host/triangle_paged_sparse_attention.cpp:122-237).
+ *
+ * workspace / workspace_bytes: device scratch of at least
+ * tm_triangle_paged_sparse_attention_workspace_size(...) bytes (may be NULL
+ * when that size is 0).  Launches that overlap in time must use distinct
+ * workspaces.
+ */
+int tm_triangle_paged_sparse_attention(
+    const void* query, const void* key_cache, const void* value_cache,
+    const int32_t* block_table, void* out,
+    int64_t query_tokens, int64_t num_pages, int64_t block_table_cols,
+    int64_t query_start, int64_t seq_len, int64_t prompt_len, float scale,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Device scratch bytes the call above needs for these arguments (0 when the
+ * whole chunk runs without split-KV partials), or -1 if the arguments are
+ * invalid (see tm_last_error).
+ * Replaces trianglemix_reference::triangle_paged_sparse_attention_workspace_size
+ * (operator/torch_adapter/triangle_paged_attention_torch.cpp:180-261).
+ */
+int64_t tm_triangle_paged_sparse_attention_workspace_size(
+    int64_t query_tokens, int64_t query_start, int64_t seq_len,
+    int64_t prompt_len);
+
+/*
+ * Dense paged causal prefill (row q attends [0, q]) built from the same
+ * tiles; serves unselected layers and fallbacks.  Replaces the dense CANN
+ * FIA call the reference falls back to
+ * (operator/tests/npu_v2_crossover.py:156-188,
+ * harness/npu_harness_common.py:278-316: TND layout, page 128,
+ * sparse_mode=3, next_tokens=0).
+ */
+int tm_dense_paged_causal_attention(
+    const void* query, const void* key_cache, const void* value_cache,
+    const int32_t* block_table, void* out,
+    int64_t query_tokens, int64_t num_pages, int64_t block_table_cols,
+    int64_t query_start, int64_t seq_len, float scale,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes for tm_dense_paged_causal_attention, or -1 if invalid. */
+int64_t tm_dense_paged_causal_attention_workspace_size(
+    int64_t query_tokens, int64_t query_start, int64_t seq_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRIANGLEMIX_H */

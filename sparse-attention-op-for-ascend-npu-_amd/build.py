@@ -1,0 +1,107 @@
+"""Build the gfx950 HIP library and its PyTorch-ROCm adapter in-tree.
+
+Outputs (next to the Python package, git-ignored, shipped with the tree):
+
+* ``trianglemix/libtrianglemix.so``        -- HIP kernels + C ABI (hipcc, gfx950)
+* ``trianglemix/_trianglemix_torch.so``    -- torch.ops registrations (g++),
+  linked to the library above through ``$ORIGIN``
+
+Usage: ``python build.py [--hip-only]``.  Each call recompiles.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+PKG = HERE / "trianglemix"
+INCLUDE = HERE.parent / "include"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = "gfx950"
+
+HIP_LIB = PKG / "libtrianglemix.so"
+TORCH_LIB = PKG / "_trianglemix_torch.so"
+
+# Disable packed fp32 VALU ops in device code (build notes).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # The host compilation pass does not know the device-only feature; that
+    # warning is expected and filtered.
+    lines = [ln for ln in proc.stdout.splitlines() if "is not a recognized feature" not in ln]
+    if proc.returncode != 0:
+        sys.stderr.write("\n".join(lines) + "\n")
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd[:3])} ...")
+    if lines:
+        sys.stdout.write("\n".join(lines) + "\n")
+
+
+def _atomic_replace(tmp: Path, dst: Path) -> None:
+    os.replace(tmp, dst)
+
+
+def build_hip_library() -> Path:
+    hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
+    tmp = HIP_LIB.with_suffix(".so.tmp")
+    _run([hipcc, *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
+          str(CSRC / "trianglemix_kernel.hip"), str(CSRC / "trianglemix_capi.cpp"),
+          "-o", str(tmp)])
+    _atomic_replace(tmp, HIP_LIB)
+    return HIP_LIB
+
+
+def build_torch_adapter() -> Path:
+    import torch
+    from torch.utils import cpp_extension
+
+    cxx = os.environ.get("CXX", "g++")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [f"-I{p}" for p in cpp_extension.include_paths()]
+    incs += [f"-I{sysconfig.get_paths()['include']}", f"-I{ROCM / 'include'}", f"-I{INCLUDE}"]
+    torch_lib = Path(cpp_extension.library_paths()[0])
+    tmp = TORCH_LIB.with_suffix(".so.tmp")
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared",
+          f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+          *incs, str(CSRC / "trianglemix_torch.cpp"),
+          f"-L{PKG}", "-ltrianglemix",
+          f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch",
+          f"-L{ROCM / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}", f"-Wl,-rpath,{ROCM / 'lib'}",
+          "-o", str(tmp)])
+    _atomic_replace(tmp, TORCH_LIB)
+    return TORCH_LIB
+
+
+def build_all(hip_only: bool = False) -> list[Path]:
+    out = [build_hip_library()]
+    if not hip_only:
+        out.append(build_torch_adapter())
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--hip-only", action="store_true")
+    args = ap.parse_args()
+    for p in build_all(args.hip_only):
+        print(f"built {p}")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,167 @@
+// C ABI of libtrianglemix.so: host-side validation and launch geometry.
+//
+// Validation restates the reference's boundary checks
+// (operator/torch_adapter/triangle_paged_attention_torch.cpp:29-97 and
+// operator/op_host/triangle_paged_sparse_attention.cpp:122-237) on plain
+// pointers and sizes.  Every check runs before any HIP call.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/trianglemix.h"
+#include "trianglemix_kernel.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+struct Range {
+  uintptr_t lo, hi;
+};
+
+bool overlaps(Range a, Range b) { return a.lo < b.hi && b.lo < a.hi; }
+
+constexpr int64_t kQueryRowBytes = int64_t(tmx::kQueryHeads) * tmx::kHeadDim * 2;
+constexpr int64_t kPageBytes = int64_t(tmx::kPageSize) * tmx::kKvHeads * tmx::kHeadDim * 2;
+
+// Attribute checks shared by the launch and workspace-size entry points.
+int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
+                     int64_t prompt_len, bool check_prompt) {
+  if (query_tokens <= 0) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "query must be [Tq, 32, 128] with Tq > 0");
+  }
+  if (query_start < 0 || seq_len <= 0 || (check_prompt && prompt_len < seq_len)) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "invalid query_start/seq_len/prompt_len/scale attributes");
+  }
+  if (query_start + query_tokens != seq_len) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "batch-one prefill requires query_start + Tq == seq_len");
+  }
+  if (seq_len > tmx::kMaxPositions || (check_prompt && prompt_len > tmx::kMaxPositions)) {
+    return fail(TM_ERR_UNSUPPORTED, "seq_len and prompt_len must not exceed %lld",
+                (long long)tmx::kMaxPositions);
+  }
+  return TM_OK;
+}
+
+int launch(bool sparse, const void* query, const void* key_cache, const void* value_cache,
+           const int32_t* block_table, void* out, int64_t query_tokens, int64_t num_pages,
+           int64_t block_table_cols, int64_t query_start, int64_t seq_len, int64_t prompt_len,
+           float scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  g_last_error[0] = '\0';
+  if (!query || !key_cache || !value_cache || !block_table || !out) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "query, key_cache, value_cache, block_table and out must be non-null");
+  }
+  int st = check_attributes(query_tokens, query_start, seq_len, prompt_len, sparse);
+  if (st != TM_OK) return st;
+  if (!std::isfinite(scale) || scale <= 0.0f) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "invalid query_start/seq_len/prompt_len/scale attributes");
+  }
+  if (num_pages <= 0 || num_pages > (int64_t(1) << 31) - 1) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "key_cache must be [pages, 128, 8, 128] with pages > 0");
+  }
+  const int64_t required_pages = (seq_len + tmx::kPageSize - 1) / tmx::kPageSize;
+  if (block_table_cols < required_pages) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "block_table lacks logical pages required by seq_len");
+  }
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace)) {
+    return fail(TM_ERR_WORKSPACE, "workspace pointer/size are inconsistent");
+  }
+  // out must not overlap any input (at::assert_no_overlap, adapter.cpp:92-96).
+  const Range r_out{(uintptr_t)out, (uintptr_t)out + uintptr_t(query_tokens * kQueryRowBytes)};
+  const Range r_q{(uintptr_t)query, (uintptr_t)query + uintptr_t(query_tokens * kQueryRowBytes)};
+  const Range r_k{(uintptr_t)key_cache, (uintptr_t)key_cache + uintptr_t(num_pages * kPageBytes)};
+  const Range r_v{(uintptr_t)value_cache, (uintptr_t)value_cache + uintptr_t(num_pages * kPageBytes)};
+  const Range r_bt{(uintptr_t)block_table, (uintptr_t)block_table + uintptr_t(block_table_cols * 4)};
+  if (overlaps(r_out, r_q) || overlaps(r_out, r_k) || overlaps(r_out, r_v) || overlaps(r_out, r_bt)) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "out must not overlap query, key_cache, value_cache or block_table");
+  }
+
+  tmx::KernelParams p{};
+  p.query = static_cast<const __bf16*>(query);
+  p.key_cache = static_cast<const __bf16*>(key_cache);
+  p.value_cache = static_cast<const __bf16*>(value_cache);
+  p.block_table = block_table;
+  p.out = static_cast<__bf16*>(out);
+  p.num_pages = (int)num_pages;
+  p.query_start = (int)query_start;
+  p.seq_len = (int)seq_len;
+  if (sparse) {
+    p.sparse_begin = tmx::kSparseBegin;
+    p.sparse_end = (int)(prompt_len > tmx::kDenseTail ? prompt_len - tmx::kDenseTail : 0);
+  } else {
+    p.sparse_begin = 0;
+    p.sparse_end = 0;
+  }
+  p.num_row_blocks = (int)((query_tokens + tmx::kQueryTile - 1) / tmx::kQueryTile);
+  p.scale_log2 = scale * 1.4426950408889634f;
+  const hipError_t err = tmx::launch_triangle_paged_attention(p, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) {
+    return fail(TM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  }
+  return TM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tm_abi_version(void) { return TM_ABI_VERSION; }
+
+const char* tm_status_string(int status) {
+  switch (status) {
+    case TM_OK: return "TM_OK";
+    case TM_ERR_INVALID_ARGUMENT: return "TM_ERR_INVALID_ARGUMENT";
+    case TM_ERR_UNSUPPORTED: return "TM_ERR_UNSUPPORTED";
+    case TM_ERR_WORKSPACE: return "TM_ERR_WORKSPACE";
+    case TM_ERR_LAUNCH: return "TM_ERR_LAUNCH";
+    default: return "TM_ERR_UNKNOWN";
+  }
+}
+
+const char* tm_last_error(void) { return g_last_error; }
+
+int tm_triangle_paged_sparse_attention(const void* query, const void* key_cache, const void* value_cache,
+                                       const int32_t* block_table, void* out, int64_t query_tokens,
+                                       int64_t num_pages, int64_t block_table_cols, int64_t query_start,
+                                       int64_t seq_len, int64_t prompt_len, float scale, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  return launch(true, query, key_cache, value_cache, block_table, out, query_tokens, num_pages,
+                block_table_cols, query_start, seq_len, prompt_len, scale, workspace, workspace_bytes, stream);
+}
+
+int64_t tm_triangle_paged_sparse_attention_workspace_size(int64_t query_tokens, int64_t query_start,
+                                                          int64_t seq_len, int64_t prompt_len) {
+  g_last_error[0] = '\0';
+  if (check_attributes(query_tokens, query_start, seq_len, prompt_len, true) != TM_OK) return -1;
+  return 0;
+}
+
+int tm_dense_paged_causal_attention(const void* query, const void* key_cache, const void* value_cache,
+                                    const int32_t* block_table, void* out, int64_t query_tokens,
+                                    int64_t num_pages, int64_t block_table_cols, int64_t query_start,
+                                    int64_t seq_len, float scale, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
+  return launch(false, query, key_cache, value_cache, block_table, out, query_tokens, num_pages,
+                block_table_cols, query_start, seq_len, seq_len, scale, workspace, workspace_bytes, stream);
+}
+
+int64_t tm_dense_paged_causal_attention_workspace_size(int64_t query_tokens, int64_t query_start,
+                                                       int64_t seq_len) {
+  g_last_error[0] = '\0';
+  if (check_attributes(query_tokens, query_start, seq_len, seq_len, false) != TM_OK) return -1;
+  return 0;
+}
+
+}  // extern "C"

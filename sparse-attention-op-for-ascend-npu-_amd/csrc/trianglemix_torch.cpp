@@ -1,0 +1,233 @@
+// PyTorch-ROCm operator boundary for libtrianglemix.so.
+//
+// Registers the reference adapter's schemas
+// (operator/torch_adapter/triangle_paged_attention_torch.cpp:265-304) for
+// ROCm device tensors (PyTorch's CUDA dispatch key on ROCm builds):
+//
+//   trianglemix_reference::triangle_paged_sparse_attention(...) -> Tensor
+//   trianglemix_reference::triangle_paged_sparse_attention_workspace_size(...) -> int
+//   trianglemix::triangle_paged_sparse_attention.out(..., *, Tensor(a!) out) -> Tensor(a!)
+//
+// plus the README's in-tree name as a positional-out alias
+//
+//   trianglemix::npu_triangle_paged_sparse_attention(..., Tensor(a!) out) -> Tensor(a!)
+//
+// and the dense paged causal companion (same tiles, no sparse rows):
+//
+//   trianglemix::dense_paged_causal_attention.out(q, k, v, bt, query_start, seq_len, scale, *, out)
+//   trianglemix_reference::dense_paged_causal_attention(q, k, v, bt, query_start, seq_len, scale)
+//
+// Input and output checks restate check_inputs / check_output (:29-97) with
+// the same predicates and messages ("GPU" for "NPU").  Launches go on the
+// current HIP stream of the query's device under a device guard, with no
+// host synchronisation.  When the library reports a non-zero workspace it is
+// taken from PyTorch's caching allocator, as the reference's EXEC_NPU_CMD
+// takes the aclnn workspace from torch_npu's allocator.
+
+#include <ATen/ATen.h>
+#include <ATen/MemoryOverlap.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "../../include/trianglemix.h"
+
+namespace trianglemix_rocm {
+namespace {
+
+void check_inputs(const at::Tensor& query, const at::Tensor& key_cache, const at::Tensor& value_cache,
+                  const at::Tensor& block_table) {
+  TORCH_CHECK(query.is_cuda(), "query must be a GPU tensor");
+  TORCH_CHECK(key_cache.is_cuda() && value_cache.is_cuda() && block_table.is_cuda(),
+              "key_cache, value_cache, and block_table must be GPU tensors");
+  TORCH_CHECK(query.scalar_type() == at::ScalarType::BFloat16, "query must be BF16");
+  TORCH_CHECK(key_cache.scalar_type() == at::ScalarType::BFloat16 &&
+                  value_cache.scalar_type() == at::ScalarType::BFloat16,
+              "key_cache and value_cache must be BF16");
+  TORCH_CHECK(block_table.scalar_type() == at::ScalarType::Int, "block_table must be INT32");
+  TORCH_CHECK(query.device() == key_cache.device() && query.device() == value_cache.device() &&
+                  query.device() == block_table.device(),
+              "all inputs must be on the same GPU device");
+  TORCH_CHECK(query.is_contiguous() && key_cache.is_contiguous() && value_cache.is_contiguous() &&
+                  block_table.is_contiguous(),
+              "all inputs must be contiguous");
+  TORCH_CHECK(query.dim() == 3 && query.size(1) == 32 && query.size(2) == 128, "query must be [Tq, 32, 128]");
+  TORCH_CHECK(key_cache.dim() == 4 && key_cache.size(1) == 128 && key_cache.size(2) == 8 &&
+                  key_cache.size(3) == 128,
+              "key_cache must be [pages, 128, 8, 128]");
+  TORCH_CHECK(value_cache.sizes() == key_cache.sizes(), "value_cache shape must equal key_cache shape");
+  TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) == 1, "block_table must be [1, max_pages]");
+}
+
+void check_output(const at::Tensor& query, const at::Tensor& key_cache, const at::Tensor& value_cache,
+                  const at::Tensor& block_table, const at::Tensor& output) {
+  TORCH_CHECK(output.is_cuda(), "out must be a GPU tensor");
+  TORCH_CHECK(output.device() == query.device(), "out must be on the same GPU device as query");
+  TORCH_CHECK(output.scalar_type() == at::ScalarType::BFloat16, "out must be BF16");
+  TORCH_CHECK(output.sizes() == query.sizes(), "out shape must exactly match query");
+  TORCH_CHECK(output.is_contiguous(), "out must be contiguous");
+  at::assert_no_internal_overlap(output);
+  at::assert_no_overlap(output, query);
+  at::assert_no_overlap(output, key_cache);
+  at::assert_no_overlap(output, value_cache);
+  at::assert_no_overlap(output, block_table);
+}
+
+void check_status(int status, const char* what) {
+  TORCH_CHECK(status == TM_OK, what, " failed (", tm_status_string(status), "): ", tm_last_error());
+}
+
+// Launch one chunk; `prompt_len < 0` selects the dense causal companion.
+void run(const at::Tensor& query, const at::Tensor& key_cache, const at::Tensor& value_cache,
+         const at::Tensor& block_table, int64_t query_start, int64_t seq_len, int64_t prompt_len, double scale,
+         at::Tensor& output) {
+  const bool sparse = prompt_len >= 0;
+  const int64_t tq = query.size(0);
+  const int64_t ws = sparse ? tm_triangle_paged_sparse_attention_workspace_size(tq, query_start, seq_len, prompt_len)
+                            : tm_dense_paged_causal_attention_workspace_size(tq, query_start, seq_len);
+  TORCH_CHECK(ws >= 0, "invalid attention attributes: ", tm_last_error());
+  at::Tensor workspace;
+  if (ws > 0) {
+    workspace = at::empty({ws}, query.options().dtype(at::kByte));
+  }
+  void* stream = c10::hip::getCurrentHIPStream(query.device().index()).stream();
+  const int status =
+      sparse ? tm_triangle_paged_sparse_attention(
+                   query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                   block_table.data_ptr<int32_t>(), output.data_ptr(), tq, key_cache.size(0), block_table.size(1),
+                   query_start, seq_len, prompt_len, static_cast<float>(scale),
+                   ws > 0 ? workspace.data_ptr() : nullptr, ws, stream)
+             : tm_dense_paged_causal_attention(
+                   query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                   block_table.data_ptr<int32_t>(), output.data_ptr(), tq, key_cache.size(0), block_table.size(1),
+                   query_start, seq_len, static_cast<float>(scale), ws > 0 ? workspace.data_ptr() : nullptr, ws,
+                   stream);
+  check_status(status, sparse ? "triangle_paged_sparse_attention" : "dense_paged_causal_attention");
+}
+
+}  // namespace
+
+at::Tensor triangle_paged_sparse_attention(const at::Tensor& query, const at::Tensor& key_cache,
+                                           const at::Tensor& value_cache, const at::Tensor& block_table,
+                                           int64_t query_start, int64_t seq_len, int64_t prompt_len, double scale) {
+  check_inputs(query, key_cache, value_cache, block_table);
+  TORCH_CHECK(prompt_len >= 0, "invalid query_start/seq_len/prompt_len/scale attributes");
+  c10::OptionalDeviceGuard guard(query.device());
+  at::Tensor output = at::empty_like(query);
+  run(query, key_cache, value_cache, block_table, query_start, seq_len, prompt_len, scale, output);
+  return output;
+}
+
+at::Tensor& triangle_paged_sparse_attention_out(const at::Tensor& query, const at::Tensor& key_cache,
+                                                const at::Tensor& value_cache, const at::Tensor& block_table,
+                                                int64_t query_start, int64_t seq_len, int64_t prompt_len,
+                                                double scale, at::Tensor& output) {
+  check_inputs(query, key_cache, value_cache, block_table);
+  check_output(query, key_cache, value_cache, block_table, output);
+  TORCH_CHECK(prompt_len >= 0, "invalid query_start/seq_len/prompt_len/scale attributes");
+  c10::OptionalDeviceGuard guard(query.device());
+  run(query, key_cache, value_cache, block_table, query_start, seq_len, prompt_len, scale, output);
+  return output;
+}
+
+int64_t triangle_paged_sparse_attention_workspace_size(const at::Tensor& query, const at::Tensor& key_cache,
+                                                       const at::Tensor& value_cache, const at::Tensor& block_table,
+                                                       int64_t query_start, int64_t seq_len, int64_t prompt_len,
+                                                       double scale) {
+  check_inputs(query, key_cache, value_cache, block_table);
+  TORCH_CHECK(std::isfinite(scale) && scale > 0.0, "invalid query_start/seq_len/prompt_len/scale attributes");
+  const int64_t ws = tm_triangle_paged_sparse_attention_workspace_size(query.size(0), query_start, seq_len, prompt_len);
+  TORCH_CHECK(ws >= 0, "triangle_paged_sparse_attention_workspace_size failed: ", tm_last_error());
+  return ws;
+}
+
+at::Tensor dense_paged_causal_attention(const at::Tensor& query, const at::Tensor& key_cache,
+                                        const at::Tensor& value_cache, const at::Tensor& block_table,
+                                        int64_t query_start, int64_t seq_len, double scale) {
+  check_inputs(query, key_cache, value_cache, block_table);
+  c10::OptionalDeviceGuard guard(query.device());
+  at::Tensor output = at::empty_like(query);
+  run(query, key_cache, value_cache, block_table, query_start, seq_len, -1, scale, output);
+  return output;
+}
+
+at::Tensor& dense_paged_causal_attention_out(const at::Tensor& query, const at::Tensor& key_cache,
+                                             const at::Tensor& value_cache, const at::Tensor& block_table,
+                                             int64_t query_start, int64_t seq_len, double scale, at::Tensor& output) {
+  check_inputs(query, key_cache, value_cache, block_table);
+  check_output(query, key_cache, value_cache, block_table, output);
+  c10::OptionalDeviceGuard guard(query.device());
+  run(query, key_cache, value_cache, block_table, query_start, seq_len, -1, scale, output);
+  return output;
+}
+
+// Shape-only implementations (the reference's InferShape: out = query shape,
+// operator/op_host/triangle_paged_sparse_attention.cpp:332-346).
+at::Tensor meta_functional(const at::Tensor& query, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
+                           int64_t, int64_t, double) {
+  return at::empty_like(query);
+}
+at::Tensor& meta_out(const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t, int64_t,
+                     int64_t, double, at::Tensor& output) {
+  return output;
+}
+at::Tensor meta_dense(const at::Tensor& query, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
+                      int64_t, double) {
+  return at::empty_like(query);
+}
+at::Tensor& meta_dense_out(const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
+                           int64_t, double, at::Tensor& output) {
+  return output;
+}
+
+}  // namespace trianglemix_rocm
+
+TORCH_LIBRARY(trianglemix_reference, ops) {
+  ops.def(
+      "triangle_paged_sparse_attention(Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor block_table, int query_start, int seq_len, int prompt_len, float scale) -> Tensor");
+  ops.def(
+      "triangle_paged_sparse_attention_workspace_size(Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor block_table, int query_start, int seq_len, int prompt_len, float scale) -> int");
+  ops.def(
+      "dense_paged_causal_attention(Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor block_table, int query_start, int seq_len, float scale) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(trianglemix_reference, CUDA, ops) {
+  ops.impl("triangle_paged_sparse_attention", &trianglemix_rocm::triangle_paged_sparse_attention);
+  ops.impl("triangle_paged_sparse_attention_workspace_size",
+           &trianglemix_rocm::triangle_paged_sparse_attention_workspace_size);
+  ops.impl("dense_paged_causal_attention", &trianglemix_rocm::dense_paged_causal_attention);
+}
+
+TORCH_LIBRARY_IMPL(trianglemix_reference, Meta, ops) {
+  ops.impl("triangle_paged_sparse_attention", &trianglemix_rocm::meta_functional);
+  ops.impl("dense_paged_causal_attention", &trianglemix_rocm::meta_dense);
+}
+
+TORCH_LIBRARY_FRAGMENT(trianglemix, ops) {
+  ops.def(
+      "triangle_paged_sparse_attention.out(Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor block_table, int query_start, int seq_len, int prompt_len, float scale, *, "
+      "Tensor(a!) out) -> Tensor(a!)");
+  ops.def(
+      "npu_triangle_paged_sparse_attention(Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor block_table, int query_start, int seq_len, int prompt_len, float scale, "
+      "Tensor(a!) out) -> Tensor(a!)");
+  ops.def(
+      "dense_paged_causal_attention.out(Tensor query, Tensor key_cache, Tensor value_cache, "
+      "Tensor block_table, int query_start, int seq_len, float scale, *, Tensor(a!) out) -> Tensor(a!)");
+}
+
+TORCH_LIBRARY_IMPL(trianglemix, CUDA, ops) {
+  ops.impl("triangle_paged_sparse_attention.out", &trianglemix_rocm::triangle_paged_sparse_attention_out);
+  ops.impl("npu_triangle_paged_sparse_attention", &trianglemix_rocm::triangle_paged_sparse_attention_out);
+  ops.impl("dense_paged_causal_attention.out", &trianglemix_rocm::dense_paged_causal_attention_out);
+}
+
+TORCH_LIBRARY_IMPL(trianglemix, Meta, ops) {
+  ops.impl("triangle_paged_sparse_attention.out", &trianglemix_rocm::meta_out);
+  ops.impl("npu_triangle_paged_sparse_attention", &trianglemix_rocm::meta_out);
+  ops.impl("dense_paged_causal_attention.out", &trianglemix_rocm::meta_dense_out);
+}

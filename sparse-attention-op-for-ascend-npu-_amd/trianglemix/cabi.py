@@ -1,0 +1,80 @@
+"""ctypes binding of the C ABI in ``include/trianglemix.h``.
+
+For callers that do not go through ``torch.ops`` (and for the parity tests,
+which exercise the C boundary directly).  Tensors are only used for their
+device pointers; the launch goes on the given stream (default: torch's
+current stream of the query's device).
+"""
+
+from __future__ import annotations
+
+from .native import load_hip_library
+
+TM_OK = 0
+TM_ERR_INVALID_ARGUMENT = 1
+TM_ERR_UNSUPPORTED = 2
+TM_ERR_WORKSPACE = 3
+TM_ERR_LAUNCH = 4
+
+
+class TriangleMixError(RuntimeError):
+    def __init__(self, status: int, message: str) -> None:
+        super().__init__(f"{message} (status {status})")
+        self.status = status
+
+
+def _check(status: int) -> None:
+    if status != TM_OK:
+        lib = load_hip_library()
+        raise TriangleMixError(status, lib.tm_last_error().decode() or lib.tm_status_string(status).decode())
+
+
+def _stream(query, stream):
+    if stream is not None:
+        return int(stream)
+    import torch
+
+    return torch.cuda.current_stream(query.device).cuda_stream
+
+
+def workspace_size(query_tokens: int, query_start: int, seq_len: int, prompt_len: int | None) -> int:
+    lib = load_hip_library()
+    if prompt_len is None:
+        n = lib.tm_dense_paged_causal_attention_workspace_size(query_tokens, query_start, seq_len)
+    else:
+        n = lib.tm_triangle_paged_sparse_attention_workspace_size(query_tokens, query_start, seq_len, prompt_len)
+    if n < 0:
+        raise TriangleMixError(TM_ERR_INVALID_ARGUMENT, lib.tm_last_error().decode())
+    return int(n)
+
+
+def _workspace(query, query_start, seq_len, prompt_len, workspace):
+    need = workspace_size(query.shape[0], query_start, seq_len, prompt_len)
+    if need == 0:
+        return None, 0
+    if workspace is None:
+        import torch
+
+        workspace = torch.empty(need, dtype=torch.uint8, device=query.device)
+    return workspace.data_ptr(), workspace.numel() * workspace.element_size()
+
+
+def triangle_paged_sparse_attention(query, key_cache, value_cache, block_table, out, *, query_start: int,
+                                    seq_len: int, prompt_len: int, scale: float, stream=None,
+                                    workspace=None) -> None:
+    lib = load_hip_library()
+    ws_ptr, ws_bytes = _workspace(query, query_start, seq_len, prompt_len, workspace)
+    _check(lib.tm_triangle_paged_sparse_attention(
+        query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(), out.data_ptr(),
+        query.shape[0], key_cache.shape[0], block_table.shape[-1], query_start, seq_len, prompt_len,
+        float(scale), ws_ptr, ws_bytes, _stream(query, stream)))
+
+
+def dense_paged_causal_attention(query, key_cache, value_cache, block_table, out, *, query_start: int,
+                                 seq_len: int, scale: float, stream=None, workspace=None) -> None:
+    lib = load_hip_library()
+    ws_ptr, ws_bytes = _workspace(query, query_start, seq_len, None, workspace)
+    _check(lib.tm_dense_paged_causal_attention(
+        query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(), out.data_ptr(),
+        query.shape[0], key_cache.shape[0], block_table.shape[-1], query_start, seq_len,
+        float(scale), ws_ptr, ws_bytes, _stream(query, stream)))

@@ -1,0 +1,222 @@
+"""Per-layer prefill routing: TriangleMix direct launch or dense fallback.
+
+Engine-independent restatement of the reference's patched
+``forward_fused_infer_attention`` decision
+(package/src/vllm_ascend_trianglemix/plugin.py:1406-1535) and its gates
+(``_dispatch_reason`` :1275-1324, ``_model_reason`` :1243-1272,
+``_validate_query`` :1134-1167, ``_validate_static_kv`` :1106-1131,
+``_validate_block_table`` :1170-1192), with the dense paged causal companion
+kernel in the role of the official FIA kernel.
+
+Order of the gates: not enabled / layer not selected / no plan -> dense
+without counters; graph capture; plan not direct (the planner's reason);
+native adapter not ready; model features (tensor / context parallel,
+non-causal, geometry, sliding window, sinks, ALiBi, encoder); query/output;
+KV cache; block table.  Any reason -> counters + dense.  A failing direct
+launch is counted as ``runtime_error_stage:direct_launch`` and re-raised in
+strict mode, else it falls back with ``DIRECT_LAUNCH_ERROR``.
+"""
+
+from __future__ import annotations
+
+import json
+import logging
+import math
+import time
+from dataclasses import dataclass
+from typing import Any, Callable
+
+from .config import PluginConfig
+from .kernel import (
+    SUPPORTED_CACHE_BLOCK_SIZE,
+    SUPPORTED_HEAD_SIZE,
+    SUPPORTED_KV_HEADS,
+    SUPPORTED_QUERY_HEADS,
+    dense_paged_causal_attention,
+    extract_layer_index,
+    triangle_direct_paged_attention,
+)
+from .native import triangle_mix_adapter_loaded
+from .planning import FallbackReason, TriangleBatchPlan
+from .stats import TriangleMixRuntimeStats, runtime_stats
+
+logger = logging.getLogger("trianglemix.router")
+
+
+@dataclass(frozen=True)
+class LayerFeatures:
+    """Model/parallel facts the reference reads from the vLLM backend."""
+
+    num_heads: int = SUPPORTED_QUERY_HEADS
+    num_kv_heads: int = SUPPORTED_KV_HEADS
+    head_size: int = SUPPORTED_HEAD_SIZE
+    causal: bool = True
+    tensor_parallel_size: int = 1
+    context_parallel: bool = False
+    sliding_window: Any = None
+    sinks: Any = None
+    alibi_slopes: Any = None
+    attn_type: str = "DECODER"
+
+
+def _dtype_name(dtype: object) -> str:
+    return str(dtype).rsplit(".", 1)[-1]
+
+
+def _contiguous(t: object) -> bool:
+    fn = getattr(t, "is_contiguous", None)
+    return bool(callable(fn) and fn())
+
+
+def _shape(t: object) -> tuple[int, ...]:
+    return tuple(int(x) for x in getattr(t, "shape", ()))
+
+
+def _model_reason(features: LayerFeatures, config: PluginConfig) -> FallbackReason:
+    if features.tensor_parallel_size != 1:
+        return FallbackReason.TENSOR_PARALLEL
+    if features.context_parallel:
+        return FallbackReason.CONTEXT_PARALLEL
+    if not features.causal:
+        return FallbackReason.NON_CAUSAL
+    if not config.kernel.has_supported_geometry:
+        return FallbackReason.GEOMETRY_UNSUPPORTED
+    if (features.sliding_window is not None or features.sinks is not None
+            or features.alibi_slopes is not None or "ENCODER" in features.attn_type.upper()):
+        return FallbackReason.MODEL_UNSUPPORTED
+    return FallbackReason.NONE
+
+
+def _query_reason(features: LayerFeatures, query: object, output: object, plan: TriangleBatchPlan) -> FallbackReason:
+    shape = _shape(query)
+    if (len(shape) != 3 or shape[1:] != (SUPPORTED_QUERY_HEADS, SUPPORTED_HEAD_SIZE)
+            or shape[0] != plan.requests[0].query_len or _dtype_name(getattr(query, "dtype", None)) != "bfloat16"
+            or not _contiguous(query) or features.num_heads != SUPPORTED_QUERY_HEADS
+            or features.num_kv_heads != SUPPORTED_KV_HEADS or features.head_size != SUPPORTED_HEAD_SIZE):
+        return FallbackReason.QUERY_UNSUPPORTED
+    oshape = _shape(output)
+    if (not oshape or oshape[0] < shape[0] or _dtype_name(getattr(output, "dtype", None)) != "bfloat16"
+            or getattr(output, "device", None) != getattr(query, "device", None) or not _contiguous(output)):
+        return FallbackReason.QUERY_UNSUPPORTED
+    return FallbackReason.NONE
+
+
+def _kv_reason(key_cache: object, value_cache: object, query: object) -> FallbackReason:
+    if key_cache is None or value_cache is None:
+        return FallbackReason.KV_CACHE_UNSUPPORTED
+    ks, vs = _shape(key_cache), _shape(value_cache)
+    if (len(ks) != 4 or ks[1:] != (SUPPORTED_CACHE_BLOCK_SIZE, SUPPORTED_KV_HEADS, SUPPORTED_HEAD_SIZE) or vs != ks
+            or _dtype_name(getattr(key_cache, "dtype", None)) != "bfloat16"
+            or _dtype_name(getattr(value_cache, "dtype", None)) != "bfloat16"
+            or getattr(key_cache, "device", None) != getattr(value_cache, "device", None)
+            or not _contiguous(key_cache) or not _contiguous(value_cache)
+            or getattr(key_cache, "device", None) != getattr(query, "device", None)):
+        return FallbackReason.KV_CACHE_UNSUPPORTED
+    return FallbackReason.NONE
+
+
+def _block_table_reason(block_table: object, query: object, seq_len: int) -> FallbackReason:
+    if block_table is None:
+        return FallbackReason.BLOCK_TABLE_UNSUPPORTED
+    shape = _shape(block_table)
+    need = math.ceil(seq_len / SUPPORTED_CACHE_BLOCK_SIZE)
+    if (len(shape) != 2 or shape[0] != 1 or shape[1] < need
+            or _dtype_name(getattr(block_table, "dtype", None)) != "int32"
+            or getattr(block_table, "device", None) != getattr(query, "device", None)
+            or not _contiguous(block_table)):
+        return FallbackReason.BLOCK_TABLE_UNSUPPORTED
+    return FallbackReason.NONE
+
+
+def dispatch_reason(*, config: PluginConfig, plan: TriangleBatchPlan, features: LayerFeatures, query: object,
+                    output: object, key_cache: object, value_cache: object, block_table: object,
+                    capturing: bool, native_ready: bool) -> FallbackReason:
+    """First failing gate for a selected layer, or ``FallbackReason.NONE``."""
+    if capturing:
+        return FallbackReason.GRAPH_CAPTURE
+    if not plan.direct:
+        return plan.primary_reason
+    if not native_ready:
+        return FallbackReason.ADAPTER_UNAVAILABLE
+    for reason in (_model_reason(features, config), _query_reason(features, query, output, plan),
+                   _kv_reason(key_cache, value_cache, query)):
+        if reason is not FallbackReason.NONE:
+            return reason
+    return _block_table_reason(block_table, query, plan.requests[0].seq_len)
+
+
+class TriangleMixRouter:
+    """Routes one layer's prefill attention for the current scheduler step.
+
+    ``direct_fn`` / ``dense_fn`` default to the gfx950 ops; tests substitute
+    them to force failure paths on the CPU.
+    """
+
+    def __init__(self, config: PluginConfig, *, stats: TriangleMixRuntimeStats | None = None,
+                 direct_fn: Callable[..., Any] = triangle_direct_paged_attention,
+                 dense_fn: Callable[..., Any] = dense_paged_causal_attention,
+                 native_ready: Callable[[], bool] = triangle_mix_adapter_loaded) -> None:
+        self.config = config
+        self.stats = stats if stats is not None else runtime_stats()
+        self.stats.configure(config.stats_recent_capacity, config.stats_log_interval)
+        self._direct = direct_fn
+        self._dense = dense_fn
+        self._native_ready = native_ready
+
+    def _dense_fallback(self, *, query, key_cache, value_cache, block_table, seq_len: int, output, scale: float):
+        view = output[: query.shape[0]]
+        return self._dense(query=query, key_cache=key_cache, value_cache=value_cache, block_table=block_table,
+                           seq_len=seq_len, output=view, softmax_scale=scale)
+
+    def _log_if_due(self) -> None:
+        payload = self.stats.structured_log_if_due()
+        if payload is not None:
+            logger.info("%s", json.dumps(payload, sort_keys=True))
+
+    def _fallback(self, plan: TriangleBatchPlan, layer_index: int | None, reason: FallbackReason) -> None:
+        # Graph-capture metadata is a reusable dummy, not a scheduled request.
+        if reason is not FallbackReason.GRAPH_CAPTURE:
+            self.stats.record_planner_decision(plan)
+        self.stats.record_layer_fallback(
+            plan_id=plan.plan_id, layer_index=layer_index, reason=reason,
+            request_indices=tuple(r.request_index for r in plan.requests[:plan.batch_size]))
+        self._log_if_due()
+
+    def prefill_attention(self, *, layer_name: str, plan: TriangleBatchPlan | None, query, key_cache, value_cache,
+                          block_table, output, softmax_scale: float, features: LayerFeatures = LayerFeatures(),
+                          capturing: bool = False):
+        """Attention of one layer for the step's chunk, written into ``output``."""
+        seq_len = plan.requests[0].seq_len if plan is not None else None
+        dense_kwargs = dict(query=query, key_cache=key_cache, value_cache=value_cache, block_table=block_table,
+                            output=output, scale=softmax_scale)
+        if not self.config.enabled or plan is None or not self.config.kernel.uses_layer(layer_name):
+            if seq_len is None:
+                raise ValueError("dense fallback needs the chunk's seq_len from a plan")
+            return self._dense_fallback(seq_len=seq_len, **dense_kwargs)
+        layer_index = extract_layer_index(layer_name)
+        reason = dispatch_reason(config=self.config, plan=plan, features=features, query=query, output=output,
+                                 key_cache=key_cache, value_cache=value_cache, block_table=block_table,
+                                 capturing=capturing, native_ready=self._native_ready())
+        if reason is not FallbackReason.NONE:
+            self._fallback(plan, layer_index, reason)
+            return self._dense_fallback(seq_len=seq_len, **dense_kwargs)
+        request = plan.requests[0]
+        rows = request.query_len
+        started = time.perf_counter_ns()
+        try:
+            self._direct(query=query[:rows], key_cache=key_cache, value_cache=value_cache, block_table=block_table,
+                         seq_len=request.seq_len, prompt_len=request.prompt_len, output=output[:rows],
+                         softmax_scale=float(softmax_scale), config=self.config.kernel)
+        except Exception:
+            self.stats.record_runtime_error(stage="direct_launch")
+            if self.config.strict:
+                raise
+            logger.exception("TriangleMix direct launch failed at layer %s; using the dense kernel", layer_name)
+            self._fallback(plan, layer_index, FallbackReason.DIRECT_LAUNCH_ERROR)
+            return self._dense_fallback(seq_len=seq_len, **dense_kwargs)
+        enqueue_ns = time.perf_counter_ns() - started
+        self.stats.record_planner_decision(plan)
+        self.stats.record_layer_dispatch(plan_id=plan.plan_id, layer_index=layer_index, saved_qk=request.saved_qk,
+                                         host_enqueue_ns=enqueue_ns, request_index=request.request_index)
+        self._log_if_due()
+        return output
