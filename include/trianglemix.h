@@ -15,8 +15,10 @@
  *
  * All pointers are device pointers; `stream` is a hipStream_t (NULL = the
  * null stream).  Every call is asynchronous: it validates its arguments on
- * the host, enqueues exactly one kernel on `stream` and returns.  No call
- * allocates device memory, synchronises, or reads device memory on the host.
+ * the host, enqueues the attention kernel on `stream` -- plus one small
+ * combine kernel when the chunk has rows long enough to split their keys
+ * across workgroups -- and returns.  No call allocates device memory,
+ * synchronises, or reads device memory on the host.
  * Arguments are validated before any HIP call, so a rejected call touches
  * no device state.
  */
@@ -63,9 +65,11 @@ const char* tm_last_error(void);
  * TilingFunc (operator/op_host/triangle_paged_sparse_attention.cpp:122-237).
  *
  * workspace / workspace_bytes: device scratch of at least
- * tm_triangle_paged_sparse_attention_workspace_size(...) bytes (may be NULL
- * when that size is 0).  Launches that overlap in time must use distinct
- * workspaces.
+ * tm_triangle_paged_sparse_attention_workspace_size(...) bytes, any content
+ * (may be NULL when that size is 0).  It receives the fp32 split-KV partials
+ * of row blocks whose keys are split across workgroups (long dense rows);
+ * launches that may overlap in time need distinct workspaces.  It must not
+ * overlap any input or out.
  */
 int tm_triangle_paged_sparse_attention(
     const void* query, const void* key_cache, const void* value_cache,

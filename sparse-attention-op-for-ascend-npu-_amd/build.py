@@ -36,6 +36,9 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Keep MFMA accumulators in VGPRs: the softmax rescales them every tile,
+    # and VALU cannot operate on AGPRs without copies.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -55,6 +55,48 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
   return TM_OK;
 }
 
+// Split-KV sizing: aim for kTargetItemsPerHead work items per KV head (two
+// 64 KB-LDS workgroups on each of the 256 CUs), and never cut a row block into
+// pieces of fewer than kMinSplitTiles tiles: a split's fp32 partial (66 KB)
+// must stay small next to the K/V it reads (32 KB per tile).
+constexpr int kTargetItemsPerHead = 64;
+constexpr int kMinSplitTiles = 16;
+
+struct Geometry {
+  int sparse_begin, sparse_end, num_row_blocks, tiles_per_split, items_per_head;
+  bool any_split;
+  int64_t workspace_bytes;
+};
+
+Geometry make_geometry(bool sparse, int64_t query_tokens, int64_t query_start, int64_t seq_len, int64_t prompt_len) {
+  Geometry g{};
+  g.sparse_begin = sparse ? tmx::kSparseBegin : 0;
+  g.sparse_end = sparse ? (int)(prompt_len > tmx::kDenseTail ? prompt_len - tmx::kDenseTail : 0) : 0;
+  g.num_row_blocks = (int)((query_tokens + tmx::kRowBlock - 1) / tmx::kRowBlock);
+  int64_t total_tiles = 0;
+  for (int o = 0; o < g.num_row_blocks; ++o) {
+    total_tiles += tmx::row_block_splits(o, g.num_row_blocks, (int)query_start, (int)seq_len, g.sparse_begin,
+                                         g.sparse_end, 1);
+  }
+  const int64_t per_item = (total_tiles + kTargetItemsPerHead - 1) / kTargetItemsPerHead;
+  g.tiles_per_split = (int)(per_item > kMinSplitTiles ? per_item : kMinSplitTiles);
+  if (g.num_row_blocks > tmx::kMaxSplitRowBlocks) {
+    g.tiles_per_split = 1 << 30;  // very long chunks run without split-KV
+  }
+  bool any_split = false;
+  int64_t items = 0;
+  for (int o = 0; o < g.num_row_blocks; ++o) {
+    const int s = tmx::row_block_splits(o, g.num_row_blocks, (int)query_start, (int)seq_len, g.sparse_begin,
+                                        g.sparse_end, g.tiles_per_split);
+    items += s;
+    any_split = any_split || s > 1;
+  }
+  g.items_per_head = (int)items;
+  g.any_split = any_split;
+  g.workspace_bytes = any_split ? int64_t(tmx::kKvHeads) * items * tmx::kPartialBytes : 0;
+  return g;
+}
+
 int launch(bool sparse, const void* query, const void* key_cache, const void* value_cache,
            const int32_t* block_table, void* out, int64_t query_tokens, int64_t num_pages,
            int64_t block_table_cols, int64_t query_start, int64_t seq_len, int64_t prompt_len,
@@ -88,25 +130,37 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
     return fail(TM_ERR_INVALID_ARGUMENT, "out must not overlap query, key_cache, value_cache or block_table");
   }
 
+  const Geometry g = make_geometry(sparse, query_tokens, query_start, seq_len, prompt_len);
+  if (workspace_bytes < g.workspace_bytes) {
+    return fail(TM_ERR_WORKSPACE, "workspace of %lld bytes is smaller than the %lld bytes this call needs",
+                (long long)workspace_bytes, (long long)g.workspace_bytes);
+  }
+  if (g.workspace_bytes > 0) {
+    const Range r_ws{(uintptr_t)workspace, (uintptr_t)workspace + uintptr_t(g.workspace_bytes)};
+    if (overlaps(r_ws, r_out) || overlaps(r_ws, r_q) || overlaps(r_ws, r_k) || overlaps(r_ws, r_v) ||
+        overlaps(r_ws, r_bt)) {
+      return fail(TM_ERR_WORKSPACE, "workspace must not overlap the inputs or out");
+    }
+  }
+
   tmx::KernelParams p{};
   p.query = static_cast<const __bf16*>(query);
   p.key_cache = static_cast<const __bf16*>(key_cache);
   p.value_cache = static_cast<const __bf16*>(value_cache);
   p.block_table = block_table;
   p.out = static_cast<__bf16*>(out);
+  p.partials = g.any_split ? static_cast<float*>(workspace) : nullptr;
   p.num_pages = (int)num_pages;
   p.query_start = (int)query_start;
   p.seq_len = (int)seq_len;
-  if (sparse) {
-    p.sparse_begin = tmx::kSparseBegin;
-    p.sparse_end = (int)(prompt_len > tmx::kDenseTail ? prompt_len - tmx::kDenseTail : 0);
-  } else {
-    p.sparse_begin = 0;
-    p.sparse_end = 0;
-  }
-  p.num_row_blocks = (int)((query_tokens + tmx::kQueryTile - 1) / tmx::kQueryTile);
+  p.sparse_begin = g.sparse_begin;
+  p.sparse_end = g.sparse_end;
+  p.num_row_blocks = g.num_row_blocks;
+  p.tiles_per_split = g.tiles_per_split;
+  p.items_per_head = g.items_per_head;
+  p.any_split = g.any_split ? 1 : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
-  const hipError_t err = tmx::launch_triangle_paged_attention(p, static_cast<hipStream_t>(stream));
+  const hipError_t err = tmx::launch_triangle_paged_attention(p, g.any_split, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     return fail(TM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   }
@@ -145,7 +199,7 @@ int64_t tm_triangle_paged_sparse_attention_workspace_size(int64_t query_tokens, 
                                                           int64_t seq_len, int64_t prompt_len) {
   g_last_error[0] = '\0';
   if (check_attributes(query_tokens, query_start, seq_len, prompt_len, true) != TM_OK) return -1;
-  return 0;
+  return make_geometry(true, query_tokens, query_start, seq_len, prompt_len).workspace_bytes;
 }
 
 int tm_dense_paged_causal_attention(const void* query, const void* key_cache, const void* value_cache,
@@ -161,7 +215,7 @@ int64_t tm_dense_paged_causal_attention_workspace_size(int64_t query_tokens, int
                                                        int64_t seq_len) {
   g_last_error[0] = '\0';
   if (check_attributes(query_tokens, query_start, seq_len, seq_len, false) != TM_OK) return -1;
-  return 0;
+  return make_geometry(false, query_tokens, query_start, seq_len, seq_len).workspace_bytes;
 }
 
 }  // extern "C"

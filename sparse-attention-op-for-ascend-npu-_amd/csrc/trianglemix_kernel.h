@@ -1,4 +1,6 @@
-// Internal interface between the C ABI host code and the gfx950 kernels.
+// Internal interface between the C ABI host code and the gfx950 kernels:
+// fixed geometry, the row-block tile schedule (shared by host and device so
+// the grid and the kernel agree exactly) and the launch parameters.
 #ifndef TRIANGLEMIX_KERNEL_H
 #define TRIANGLEMIX_KERNEL_H
 
@@ -19,10 +21,55 @@ constexpr int kSinkTokens = 8;
 constexpr int kLocalWindow = 512;
 constexpr int kDenseTail = 128;
 constexpr int kSparseBegin = kSinkTokens + kLocalWindow + 1;  // 521
-constexpr int kKvTile = 64;  // keys per LDS tile (divides the 128-token page)
+
+// Kernel tiling.
+constexpr int kKvTile = 64;    // keys per LDS tile (divides the 128-token page)
+constexpr int kRowBlock = 32;  // query tokens per work item (x 4 GQA heads = 128 rows)
+// One split-KV partial, fp32, per wave (query head) and lane: 64 O values,
+// the row max and the lane's partial row sum.
+constexpr int64_t kPartialFloats = int64_t(kGroup) * 64 * (64 + 2);
+constexpr int64_t kPartialBytes = kPartialFloats * 4;
+// Row blocks with more than this many rows are never split (bounds the
+// combine kernel's grid and keeps position arithmetic in 32 bits).
+constexpr int kMaxSplitRowBlocks = 1 << 20;
 
 // Largest seq_len / prompt_len the 32-bit position arithmetic accepts.
 constexpr int64_t kMaxPositions = (int64_t(1) << 30);
+
+// Tile schedule of one row block [tb, te): up to two runs of 64-key tiles.
+// A block whose rows are all sparse visits the sink tile plus the tiles of
+// [tb - 512, te); any other block visits [0, te).
+struct TileRuns {
+  int first0, count0, first1, count1;
+  __host__ __device__ int count() const { return count0 + count1; }
+  __host__ __device__ int tile(int i) const { return i < count0 ? first0 + i : first1 + (i - count0); }
+};
+
+__host__ __device__ inline TileRuns row_block_tiles(int tb, int te, int sparse_begin, int sparse_end) {
+  TileRuns r{0, 0, 0, 0};
+  const int last = (te - 1) / kKvTile;
+  const bool all_sparse = tb >= sparse_begin && te <= sparse_end;
+  const int local_first = all_sparse ? (tb - kLocalWindow) / kKvTile : 0;  // tb >= 521 when all sparse
+  if (local_first <= 0) {
+    r.count0 = last + 1;
+  } else {
+    r.count0 = 1;  // sink tile [0, 64)
+    r.first1 = local_first;
+    r.count1 = last - local_first + 1;
+  }
+  return r;
+}
+
+// Row blocks are issued last-first (later rows attend more keys): order
+// index o is row block num_row_blocks - 1 - o.
+__host__ __device__ inline int row_block_splits(int o, int num_row_blocks, int query_start, int seq_len,
+                                                int sparse_begin, int sparse_end, int tiles_per_split) {
+  const int rb = num_row_blocks - 1 - o;
+  const int tb = query_start + rb * kRowBlock;
+  const int te = tb + kRowBlock < seq_len ? tb + kRowBlock : seq_len;
+  const int n = row_block_tiles(tb, te, sparse_begin, sparse_end).count();
+  return (n + tiles_per_split - 1) / tiles_per_split;
+}
 
 struct KernelParams {
   const __bf16* query;        // [tq, 32, 128]
@@ -30,16 +77,22 @@ struct KernelParams {
   const __bf16* value_cache;  // [num_pages, 128, 8, 128]
   const int32_t* block_table; // [>= ceil(seq_len/128)]
   __bf16* out;                // [tq, 32, 128]
+  float* partials;            // [8][items_per_head] split-KV partials, or null
   int num_pages;
   int query_start;
   int seq_len;
-  int sparse_begin;  // 521 for TriangleMix, 0 for dense causal
-  int sparse_end;    // max(0, prompt_len-128) for TriangleMix, 0 for dense causal
+  int sparse_begin;    // 521 for TriangleMix, 0 for dense causal
+  int sparse_end;      // max(0, prompt_len-128) for TriangleMix, 0 for dense causal
   int num_row_blocks;
-  float scale_log2;  // softmax scale * log2(e)
+  int tiles_per_split; // max 64-key tiles per work item
+  int items_per_head;  // sum over row blocks of their split counts
+  int any_split;       // 0: every row block is one item (item index = row-block order)
+  float scale_log2;    // softmax scale * log2(e)
 };
 
-hipError_t launch_triangle_paged_attention(const KernelParams& p, hipStream_t stream);
+// Enqueues the attention kernel and, when some row block is split, the
+// combine kernel that merges its partials (same stream, in order).
+hipError_t launch_triangle_paged_attention(const KernelParams& p, bool any_split, hipStream_t stream);
 
 }  // namespace tmx
 

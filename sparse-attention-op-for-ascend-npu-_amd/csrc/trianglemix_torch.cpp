@@ -20,9 +20,10 @@
 // Input and output checks restate check_inputs / check_output (:29-97) with
 // the same predicates and messages ("GPU" for "NPU").  Launches go on the
 // current HIP stream of the query's device under a device guard, with no
-// host synchronisation.  When the library reports a non-zero workspace it is
-// taken from PyTorch's caching allocator, as the reference's EXEC_NPU_CMD
-// takes the aclnn workspace from torch_npu's allocator.
+// host synchronisation.  When the library reports a non-zero split-KV
+// workspace it is taken from PyTorch's caching allocator for the call, as the
+// reference's EXEC_NPU_CMD takes the aclnn workspace from torch_npu's
+// allocator (stream-ordered reuse keeps it valid until the kernels finish).
 
 #include <ATen/ATen.h>
 #include <ATen/MemoryOverlap.h>
@@ -86,21 +87,20 @@ void run(const at::Tensor& query, const at::Tensor& key_cache, const at::Tensor&
   const int64_t ws = sparse ? tm_triangle_paged_sparse_attention_workspace_size(tq, query_start, seq_len, prompt_len)
                             : tm_dense_paged_causal_attention_workspace_size(tq, query_start, seq_len);
   TORCH_CHECK(ws >= 0, "invalid attention attributes: ", tm_last_error());
-  at::Tensor workspace;
-  if (ws > 0) {
-    workspace = at::empty({ws}, query.options().dtype(at::kByte));
-  }
   void* stream = c10::hip::getCurrentHIPStream(query.device().index()).stream();
+  at::Tensor ws_tensor;
+  if (ws > 0) ws_tensor = at::empty({ws}, query.options().dtype(at::kByte));
+  void* workspace = ws > 0 ? ws_tensor.data_ptr() : nullptr;
   const int status =
       sparse ? tm_triangle_paged_sparse_attention(
                    query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
                    block_table.data_ptr<int32_t>(), output.data_ptr(), tq, key_cache.size(0), block_table.size(1),
                    query_start, seq_len, prompt_len, static_cast<float>(scale),
-                   ws > 0 ? workspace.data_ptr() : nullptr, ws, stream)
+                   workspace, ws, stream)
              : tm_dense_paged_causal_attention(
                    query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
                    block_table.data_ptr<int32_t>(), output.data_ptr(), tq, key_cache.size(0), block_table.size(1),
-                   query_start, seq_len, static_cast<float>(scale), ws > 0 ? workspace.data_ptr() : nullptr, ws,
+                   query_start, seq_len, static_cast<float>(scale), workspace, ws,
                    stream);
   check_status(status, sparse ? "triangle_paged_sparse_attention" : "dense_paged_causal_attention");
 }

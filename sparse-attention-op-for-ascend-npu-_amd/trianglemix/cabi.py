@@ -48,7 +48,7 @@ def workspace_size(query_tokens: int, query_start: int, seq_len: int, prompt_len
     return int(n)
 
 
-def _workspace(query, query_start, seq_len, prompt_len, workspace):
+def _workspace(query, query_start, seq_len, prompt_len, workspace, stream):
     need = workspace_size(query.shape[0], query_start, seq_len, prompt_len)
     if need == 0:
         return None, 0
@@ -63,18 +63,20 @@ def triangle_paged_sparse_attention(query, key_cache, value_cache, block_table, 
                                     seq_len: int, prompt_len: int, scale: float, stream=None,
                                     workspace=None) -> None:
     lib = load_hip_library()
-    ws_ptr, ws_bytes = _workspace(query, query_start, seq_len, prompt_len, workspace)
+    st = _stream(query, stream)
+    ws_ptr, ws_bytes = _workspace(query, query_start, seq_len, prompt_len, workspace, st)
     _check(lib.tm_triangle_paged_sparse_attention(
         query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(), out.data_ptr(),
         query.shape[0], key_cache.shape[0], block_table.shape[-1], query_start, seq_len, prompt_len,
-        float(scale), ws_ptr, ws_bytes, _stream(query, stream)))
+        float(scale), ws_ptr, ws_bytes, st))
 
 
 def dense_paged_causal_attention(query, key_cache, value_cache, block_table, out, *, query_start: int,
                                  seq_len: int, scale: float, stream=None, workspace=None) -> None:
     lib = load_hip_library()
-    ws_ptr, ws_bytes = _workspace(query, query_start, seq_len, None, workspace)
+    st = _stream(query, stream)
+    ws_ptr, ws_bytes = _workspace(query, query_start, seq_len, None, workspace, st)
     _check(lib.tm_dense_paged_causal_attention(
         query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(), out.data_ptr(),
         query.shape[0], key_cache.shape[0], block_table.shape[-1], query_start, seq_len,
-        float(scale), ws_ptr, ws_bytes, _stream(query, stream)))
+        float(scale), ws_ptr, ws_bytes, st))

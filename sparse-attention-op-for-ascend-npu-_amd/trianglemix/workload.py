@@ -95,7 +95,7 @@ def kv_bytes(c: Chunk, *, dense: bool = False) -> int:
 
 
 KV_TILE = 64   # keys per kernel tile
-ROW_BLOCK = 32  # query tokens per workgroup
+ROW_BLOCK = 32  # query tokens per work item
 
 
 def executed_tiles(c: Chunk, *, dense: bool = False) -> int:

@@ -233,3 +233,50 @@ def test_deterministic_and_page_permutation_invariant(gpu):
     bt2 = torch.tensor([new_table], dtype=torch.int32)
     c = _run_sparse(q, k2, v2, bt2, qs, seq, prompt, gpu)
     assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("qs,tq,seq,prompt", [(1000, 37, 1037, 2048), (600, 300, 900, 4000), (0, 70, 70, 70)])
+def test_garbage_beyond_seq_len_is_never_read(gpu, qs, tq, seq, prompt):
+    """Slots past seq_len (tail of the last page, unused physical pages) hold NaN;
+    the result must equal the clean-cache result bit for bit."""
+    q, k, v, bt = make_inputs(qs, tq, seq, 555 + tq)
+    clean = _run_sparse(q, k, v, bt, qs, seq, prompt, gpu)
+    table = bt[0].tolist()
+    used = set(table[: math.ceil(seq / 128)])
+    k2, v2 = k.clone(), v.clone()
+    nan = float("nan")
+    for page in range(k.shape[0]):
+        if page not in used:
+            k2[page].fill_(nan)
+            v2[page].fill_(nan)
+    last_page, last_off = OG.physical_location(seq - 1, table)
+    k2[last_page, last_off + 1:].fill_(nan)
+    v2[last_page, last_off + 1:].fill_(nan)
+    dirty = _run_sparse(q, k2, v2, bt, qs, seq, prompt, gpu)
+    assert torch.isfinite(dirty.float()).all()
+    assert torch.equal(clean, dirty)
+
+
+def test_workspace_reuse_across_geometries(gpu):
+    """One workspace reused by calls with different row-block and split counts
+    (dirty from the previous call); every call must match its own result on a
+    fresh workspace filled with NaN."""
+    shapes = [(8192, 128, 8320, 8320), (0, 512, 512, 512), (7680, 512, 8192, 8192), (100, 1400, 1500, 1600),
+              (0, 512, 512, 512), (8192, 128, 8320, 8320)]
+    k, v, bt = make_cache(8320, 91)
+    kd, vd, btd = k.to(gpu), v.to(gpu), bt.to(gpu)
+    shared = torch.full((256 << 20,), 0xFF, dtype=torch.uint8, device=gpu)
+    for qs, tq, seq, prompt in shapes:
+        q = make_query(tq, qs + 1).to(gpu)
+        need = cabi.workspace_size(tq, qs, seq, prompt)
+        assert need <= shared.numel()
+        a = torch.full_like(q, float("nan"))
+        cabi.triangle_paged_sparse_attention(q, kd, vd, btd, a, query_start=qs, seq_len=seq, prompt_len=prompt,
+                                             scale=SCALE, workspace=shared)
+        fresh = torch.full((max(need, 1),), 0xFF, dtype=torch.uint8, device=gpu)
+        b = torch.full_like(q, float("nan"))
+        cabi.triangle_paged_sparse_attention(q, kd, vd, btd, b, query_start=qs, seq_len=seq, prompt_len=prompt,
+                                             scale=SCALE, workspace=fresh)
+        torch.cuda.synchronize()
+        assert torch.isfinite(a.float()).all(), (qs, tq)
+        assert torch.equal(a, b), (qs, tq)
