@@ -70,13 +70,13 @@ def unique_kv_tokens(c: Chunk, *, dense: bool = False) -> int:
     if dense:
         return q1
     s0, s1 = _sparse_range(q0, q1, c.prompt_len)
+    if s1 <= s0:  # no sparse rows: every row is causal-dense
+        return q1
     dense_rows_max = -1
     if q0 < s0:
         dense_rows_max = s0 - 1
     if s1 < q1:
         dense_rows_max = q1 - 1
-    if s1 <= s0:  # no sparse rows
-        return dense_rows_max + 1
     lo, hi = s0 - WINDOW, s1  # local band of the sparse rows
     if dense_rows_max >= 0:
         n = dense_rows_max + 1

@@ -1,0 +1,201 @@
+"""The drop-in boundary on the CPU: the C-ABI library and the torch adapter.
+
+No kernel runs here.  Checks:
+
+* ``libtrianglemix.so`` loads and exports every function ``include/trianglemix.h``
+  declares, with the declared ABI version and status strings;
+* every validation error of the launch entry points is returned before any
+  HIP call (fake, never-dereferenced pointers; the attributes are invalid, so
+  no launch is attempted);
+* the workspace-size entry points: zero when no row block is split, whole
+  per-item partial records otherwise, -1 on invalid attributes;
+* the torch adapter registers the reference's exact schema strings
+  (operator/torch_adapter/triangle_paged_attention_torch.cpp:264-296) plus the
+  ``npu_triangle_paged_sparse_attention`` alias, shape-infers on the Meta
+  device, and has no CPU kernel (a CPU call fails loudly instead of falling
+  back).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from trianglemix import cabi, native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "trianglemix.h"
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+PARTIAL_BYTES = 4 * 64 * 66 * 4  # fp32 partial record of one (row block, kv head, split) item
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not native.HIP_LIBRARY.is_file() or not native.TORCH_ADAPTER.is_file():
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("tm_build", native.PKG_DIR.parent / "build.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build_all()
+    return native.load_hip_library()
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(tm_[a-z_]+)\s*\(", text)))
+
+
+def test_header_functions_are_exported(lib):
+    names = _declared_functions()
+    assert names == sorted([
+        "tm_abi_version", "tm_status_string", "tm_last_error",
+        "tm_triangle_paged_sparse_attention", "tm_triangle_paged_sparse_attention_workspace_size",
+        "tm_dense_paged_causal_attention", "tm_dense_paged_causal_attention_workspace_size"])
+    raw = ctypes.CDLL(str(native.HIP_LIBRARY))
+    for name in names:
+        assert getattr(raw, name) is not None, name
+
+
+def test_abi_version_and_status_strings(lib):
+    m = re.search(r"#define\s+TM_ABI_VERSION\s+(\d+)", HEADER.read_text())
+    assert lib.tm_abi_version() == int(m.group(1)) == native.ABI_VERSION
+    for code, name in [(0, "TM_OK"), (1, "TM_ERR_INVALID_ARGUMENT"), (2, "TM_ERR_UNSUPPORTED"),
+                       (3, "TM_ERR_WORKSPACE"), (4, "TM_ERR_LAUNCH"), (99, "TM_ERR_UNKNOWN")]:
+        assert lib.tm_status_string(code).decode() == name
+        if code < 5:
+            assert re.search(rf"#define\s+{name}\s+{code}\b", HEADER.read_text())
+
+
+# fake device addresses, far apart; never dereferenced because every call below fails validation
+Q, K, V, BT, OUT, WS = (0x10_0000_0000 * (i + 1) for i in range(6))
+GOOD = dict(query=Q, key=K, value=V, table=BT, out=OUT, tq=512, pages=71, cols=64, qs=4096, seq=4608, prompt=8192,
+            scale=0.08838834764831845, ws=0, ws_bytes=0)
+
+
+def _sparse(lib, **over):
+    a = dict(GOOD, **over)
+    return lib.tm_triangle_paged_sparse_attention(a["query"], a["key"], a["value"], a["table"], a["out"], a["tq"],
+                                                  a["pages"], a["cols"], a["qs"], a["seq"], a["prompt"], a["scale"],
+                                                  a["ws"], a["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(query=None), 1, "non-null"),
+    (dict(out=None), 1, "non-null"),
+    (dict(tq=0, qs=4608), 1, "Tq > 0"),
+    (dict(qs=4000), 1, "query_start \\+ Tq == seq_len"),
+    (dict(prompt=4000), 1, "prompt_len"),
+    (dict(scale=0.0), 1, "scale"),
+    (dict(scale=float("nan")), 1, "scale"),
+    (dict(scale=float("inf")), 1, "scale"),
+    (dict(pages=0), 1, "pages > 0"),
+    (dict(cols=35), 1, "block_table lacks"),
+    (dict(out=Q + 1024), 1, "must not overlap"),
+    (dict(out=K + 4096), 1, "must not overlap"),
+    (dict(out=BT), 1, "must not overlap"),
+    (dict(ws=0, ws_bytes=4096), 3, "inconsistent"),
+    (dict(ws_bytes=-1, ws=WS), 3, "inconsistent"),
+    (dict(tq=512, qs=(1 << 30), seq=(1 << 30) + 512, prompt=(1 << 30) + 512, cols=(1 << 23) + 4), 2, "exceed"),
+])
+def test_sparse_entry_validation_errors(lib, over, status, msg):
+    assert _sparse(lib, **over) == status
+    assert re.search(msg, lib.tm_last_error().decode()), lib.tm_last_error()
+
+
+def test_small_workspace_is_rejected_before_launch(lib):
+    need = lib.tm_triangle_paged_sparse_attention_workspace_size(512, 7680, 8192, 8192)
+    assert need > 0
+    assert _sparse(lib, qs=7680, seq=8192, ws=WS, ws_bytes=need - 1) == 3
+    assert "smaller than" in lib.tm_last_error().decode()
+    assert _sparse(lib, qs=7680, seq=8192, ws=OUT - 16, ws_bytes=need) == 3  # workspace overlapping out
+    assert "overlap" in lib.tm_last_error().decode()
+
+
+def test_dense_entry_validation_errors(lib):
+    r = lib.tm_dense_paged_causal_attention(Q, K, V, BT, OUT, 512, 71, 64, 4000, 4608, 0.088, 0, 0, None)
+    assert r == 1 and "query_start + Tq" in lib.tm_last_error().decode()
+    r = lib.tm_dense_paged_causal_attention(Q, K, V, BT, None, 512, 71, 64, 4096, 4608, 0.088, 0, 0, None)
+    assert r == 1
+
+
+def test_workspace_sizes(lib):
+    ws = lib.tm_triangle_paged_sparse_attention_workspace_size
+    dws = lib.tm_dense_paged_causal_attention_workspace_size
+    # sparse middle chunks: every row block holds few tiles -> no split, no workspace
+    assert ws(512, 4096, 4608, 8192) == 0
+    assert ws(5, 250, 255, 2048) == 0
+    # long rows (dense tail, dense companion) are split over KV -> whole partial records for 8 KV heads
+    for n in (ws(512, 7680, 8192, 8192), dws(512, 7680, 8192), dws(2048, 6272, 8320)):
+        assert n > 0 and n % (8 * PARTIAL_BYTES) == 0
+    assert dws(512, 7680, 8192) >= ws(512, 7680, 8192, 8192)
+    # invalid attributes -> -1 with a message
+    assert ws(0, 0, 0, 0) == -1 and lib.tm_last_error().decode()
+    assert ws(512, 4096, 4608, 4000) == -1
+    assert dws(512, 4000, 4608) == -1
+
+
+def test_cabi_workspace_size_wrapper(lib):
+    assert cabi.workspace_size(512, 4096, 4608, 8192) == 0
+    with pytest.raises(cabi.TriangleMixError):
+        cabi.workspace_size(512, 4000, 4608, 8192)
+
+
+# ------------------------------------------------------------ torch adapter
+
+@pytest.fixture(scope="module")
+def adapter(lib):
+    native.load_triangle_mix_adapter()
+    return torch.ops
+
+
+def test_adapter_schemas_match_reference(adapter):
+    schemas = KATS["op_schemas"]
+    got = {
+        "trianglemix_reference::triangle_paged_sparse_attention":
+            adapter.trianglemix_reference.triangle_paged_sparse_attention.default._schema,
+        "trianglemix_reference::triangle_paged_sparse_attention_workspace_size":
+            adapter.trianglemix_reference.triangle_paged_sparse_attention_workspace_size.default._schema,
+        "trianglemix::triangle_paged_sparse_attention.out":
+            adapter.trianglemix.triangle_paged_sparse_attention.out._schema,
+    }
+    for name, schema in got.items():
+        assert str(schema) == schemas[name], name
+    alias = str(adapter.trianglemix.npu_triangle_paged_sparse_attention.default._schema)
+    assert "Tensor(a!) out) -> Tensor(a!)" in alias and "int prompt_len, float scale" in alias
+
+
+def test_adapter_load_is_idempotent_and_refuses_second_path(adapter, tmp_path):
+    assert native.load_triangle_mix_adapter() == native.load_triangle_mix_adapter()
+    other = tmp_path / "other.so"
+    other.write_bytes(b"")
+    with pytest.raises(RuntimeError, match="refusing"):
+        native.load_triangle_mix_adapter(other)
+    assert native.native_status().ready
+
+
+def test_meta_shape_inference(adapter):
+    q = torch.empty(512, 32, 128, dtype=torch.bfloat16, device="meta")
+    k = torch.empty(71, 128, 8, 128, dtype=torch.bfloat16, device="meta")
+    bt = torch.empty(1, 64, dtype=torch.int32, device="meta")
+    out = adapter.trianglemix_reference.triangle_paged_sparse_attention(q, k, k, bt, 4096, 4608, 8192, 0.088)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16 and out.device.type == "meta"
+    o2 = torch.empty_like(q)
+    assert adapter.trianglemix.triangle_paged_sparse_attention.out(q, k, k, bt, 4096, 4608, 8192, 0.088,
+                                                                    out=o2) is o2
+
+
+def test_cpu_tensors_have_no_kernel(adapter):
+    q = torch.zeros(4, 32, 128, dtype=torch.bfloat16)
+    k = torch.zeros(2, 128, 8, 128, dtype=torch.bfloat16)
+    bt = torch.zeros(1, 2, dtype=torch.int32)
+    with pytest.raises(NotImplementedError):
+        adapter.trianglemix.triangle_paged_sparse_attention.out(q, k, k, bt, 0, 4, 1024, 0.088,
+                                                                 out=torch.empty_like(q))
+    with pytest.raises(NotImplementedError):
+        adapter.trianglemix_reference.dense_paged_causal_attention(q, k, k, bt, 0, 4, 0.088)
