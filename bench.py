@@ -1,6 +1,6 @@
 """Benchmark: TriangleMix sparse prefill attention on one MI355X.
 
-Workload: Qwen3-8B attention geometry (Hq=32, Hkv=8,
+Workload (the headline configuration): Qwen3-8B attention geometry (Hq=32, Hkv=8,
 D=128, bf16, page 128), one request, prompt L=8192 prefilled in 16 chunks of
 512.  One *step* = the 16 chunk launches of the sparse kernel, in order, over
 one paged K/V cache (random block-table permutation) that already holds the
@@ -42,7 +42,7 @@ for _p in (ROOT, PKG_ROOT):
 METRIC = "sparse-prefill attn µs/chunk + MFMA %peak, Qwen3-8B GQA, L=8192 chunk 512"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
-TRAFFIC_SUMMARY = ROOT / "profiles" / "traffic_triangle_config2.json"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "triangle_config2_traffic.md"
 
 
 def parse_args() -> argparse.Namespace:
@@ -56,6 +56,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--only", choices=("sparse", "dense"), help="run one kernel only (for profiling)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run 5 plain device copies of MIB MiB (scales rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -63,7 +65,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported; this build measures one MI355X "
-              "(the op has no cross-GPU path; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the op has no cross-GPU path)", file=sys.stderr)
         return 2
 
     import torch
@@ -179,12 +181,15 @@ def main() -> int:
     us_per_chunk = ms_sparse * 1000.0 / n
     achieved_tflops = alg_flops / (ms_sparse * 1e-3) / 1e12
 
-    traffic = None
-    if TRAFFIC_SUMMARY.is_file():
-        try:
-            traffic = json.loads(TRAFFIC_SUMMARY.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
+    if args.copy_calibration > 0:
+        src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    traffic = read_traffic_summary()
 
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
@@ -231,6 +236,19 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def read_traffic_summary():
+    """HBM bytes per launch of the attention kernel from the committed rocprofv3 summary, or None."""
+    if not TRAFFIC_SUMMARY.is_file():
+        return None
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            try:
+                return int(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
 
 
 def cpu_baseline(chunks, qfull, k, v, bt, scale):

@@ -29,7 +29,8 @@ ARCH = "gfx950"
 HIP_LIB = PKG / "libtrianglemix.so"
 TORCH_LIB = PKG / "_trianglemix_torch.so"
 
-# Disable packed fp32 VALU ops in device code (build notes).
+# Disable packed fp32 VALU ops in device code: some of their forms have given
+# wrong results on this hardware class, silently.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

@@ -55,15 +55,21 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
   return TM_OK;
 }
 
-// Split-KV sizing: aim for kTargetItemsPerHead work items per KV head (two
-// 64 KB-LDS workgroups on each of the 256 CUs), and never cut a row block into
+// Split-KV sizing: aim for kTargetItemsPerHead work items per KV head (each
+// item runs as two workgroups, so 32 items per head make two rounds of
+// workgroups over the 256 CUs), and never cut a row block into
 // pieces of fewer than kMinSplitTiles tiles: a split's fp32 partial (66 KB)
 // must stay small next to the K/V it reads (32 KB per tile).
-constexpr int kTargetItemsPerHead = 64;
+constexpr int kTargetItemsPerHead = 32;
 constexpr int kMinSplitTiles = 16;
 
+// Work items per KV head beyond which a launch is refused (its grid would
+// exceed 2^30 workgroups).
+constexpr int64_t kMaxItemsPerHead = int64_t(1) << 26;
+
 struct Geometry {
-  int sparse_begin, sparse_end, num_row_blocks, tiles_per_split, items_per_head;
+  int sparse_begin, sparse_end, num_row_blocks, tiles_per_split;
+  int64_t items_per_head;
   bool any_split;
   int64_t workspace_bytes;
 };
@@ -80,9 +86,7 @@ Geometry make_geometry(bool sparse, int64_t query_tokens, int64_t query_start, i
   }
   const int64_t per_item = (total_tiles + kTargetItemsPerHead - 1) / kTargetItemsPerHead;
   g.tiles_per_split = (int)(per_item > kMinSplitTiles ? per_item : kMinSplitTiles);
-  if (g.num_row_blocks > tmx::kMaxSplitRowBlocks) {
-    g.tiles_per_split = 1 << 30;  // very long chunks run without split-KV
-  }
+  if (g.tiles_per_split > tmx::kMaxItemTiles) g.tiles_per_split = tmx::kMaxItemTiles;
   bool any_split = false;
   int64_t items = 0;
   for (int o = 0; o < g.num_row_blocks; ++o) {
@@ -91,7 +95,7 @@ Geometry make_geometry(bool sparse, int64_t query_tokens, int64_t query_start, i
     items += s;
     any_split = any_split || s > 1;
   }
-  g.items_per_head = (int)items;
+  g.items_per_head = items;
   g.any_split = any_split;
   g.workspace_bytes = any_split ? int64_t(tmx::kKvHeads) * items * tmx::kPartialBytes : 0;
   return g;
@@ -131,6 +135,10 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   }
 
   const Geometry g = make_geometry(sparse, query_tokens, query_start, seq_len, prompt_len);
+  if (g.items_per_head > kMaxItemsPerHead) {
+    return fail(TM_ERR_UNSUPPORTED, "chunk needs %lld work items per KV head; the limit is %lld",
+                (long long)g.items_per_head, (long long)kMaxItemsPerHead);
+  }
   if (workspace_bytes < g.workspace_bytes) {
     return fail(TM_ERR_WORKSPACE, "workspace of %lld bytes is smaller than the %lld bytes this call needs",
                 (long long)workspace_bytes, (long long)g.workspace_bytes);
@@ -157,10 +165,11 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   p.sparse_end = g.sparse_end;
   p.num_row_blocks = g.num_row_blocks;
   p.tiles_per_split = g.tiles_per_split;
-  p.items_per_head = g.items_per_head;
+  p.items_per_head = (int)g.items_per_head;
   p.any_split = g.any_split ? 1 : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
-  const hipError_t err = tmx::launch_triangle_paged_attention(p, g.any_split, static_cast<hipStream_t>(stream));
+  const hipError_t err =
+      tmx::launch_triangle_paged_attention(p, sparse, g.any_split, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     return fail(TM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   }

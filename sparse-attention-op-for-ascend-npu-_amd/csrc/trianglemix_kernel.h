@@ -24,14 +24,15 @@ constexpr int kSparseBegin = kSinkTokens + kLocalWindow + 1;  // 521
 
 // Kernel tiling.
 constexpr int kKvTile = 64;    // keys per LDS tile (divides the 128-token page)
-constexpr int kRowBlock = 32;  // query tokens per work item (x 4 GQA heads = 128 rows)
-// One split-KV partial, fp32, per wave (query head) and lane: 64 O values,
-// the row max and the lane's partial row sum.
+constexpr int kRowBlock = 32;  // query tokens per work item
+// One split-KV partial per (KV head, work item), fp32, for each of the 4
+// query heads and 64 lanes: 64 O values, the row max and the lane's partial
+// row sum.
 constexpr int64_t kPartialFloats = int64_t(kGroup) * 64 * (64 + 2);
 constexpr int64_t kPartialBytes = kPartialFloats * 4;
-// Row blocks with more than this many rows are never split (bounds the
-// combine kernel's grid and keeps position arithmetic in 32 bits).
-constexpr int kMaxSplitRowBlocks = 1 << 20;
+// Largest number of 64-key tiles one work item may hold: the kernel keeps the
+// item's page numbers in two 64-lane registers.  Longer rows are split.
+constexpr int kMaxItemTiles = 128;
 
 // Largest seq_len / prompt_len the 32-bit position arithmetic accepts.
 constexpr int64_t kMaxPositions = (int64_t(1) << 30);
@@ -90,9 +91,10 @@ struct KernelParams {
   float scale_log2;    // softmax scale * log2(e)
 };
 
-// Enqueues the attention kernel and, when some row block is split, the
-// combine kernel that merges its partials (same stream, in order).
-hipError_t launch_triangle_paged_attention(const KernelParams& p, bool any_split, hipStream_t stream);
+// Enqueues the attention kernel (TriangleMix mask when `sparse`, plain causal
+// otherwise) and, when some row block is split, the combine kernel that
+// merges its partials (same stream, in order).
+hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, bool any_split, hipStream_t stream);
 
 }  // namespace tmx
 

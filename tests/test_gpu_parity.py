@@ -2,11 +2,11 @@
 
 Called through the C ABI (``trianglemix.cabi`` -> ``libtrianglemix.so``).
 Cases: the reference's 18-case boundary matrix and its two sentinels
-(operator/tests/npu_v2_correctness.py:53-216, :401-523), BASELINE config 1,
+(operator/tests/npu_v2_correctness.py:53-216, :401-523), the L=2869 config,
 the full config-2 prefill, ragged / unaligned chunks, the dense companion,
 and an exact mask-identity probe.
 
-Tolerances (tighter than the reference's 0.05 / 0.005):
+Tolerances (the project's target, tighter than the reference's 0.05 / 0.005):
 max-abs <= 2e-2, mean-abs <= 2e-3, relative L2 <= 2e-2 against fp32.
 """
 
@@ -134,7 +134,7 @@ def test_gqa_sentinel(gpu):
 
 
 def test_config1_last_chunk(gpu):
-    """L=2869, rows 2357..2868 (384 sparse + 128 dense tail)."""
+    """Config 1: L=2869, rows 2357..2868 (384 sparse + 128 dense tail)."""
     q, k, v, bt = make_inputs(2357, 512, 2869, 1, std=1.0)
     expected = OA.attention_torch(q, k, v, bt, 2357, 2869, 2869, SCALE)
     actual = _run_sparse(q, k, v, bt, 2357, 2869, 2869, gpu)
@@ -142,7 +142,7 @@ def test_config1_last_chunk(gpu):
 
 
 def test_config2_full_prefill(gpu):
-    """L=8192, 16 chunks of 512 in order over one paged cache."""
+    """Config 2: L=8192, 16 chunks of 512 in order over one paged cache."""
     k, v, bt = make_cache(8192, 7, std=1.0)
     qfull = make_query(8192, 8, std=1.0)
     kd, vd, btd = k.to(gpu), v.to(gpu), bt.to(gpu)
@@ -161,7 +161,7 @@ def test_config2_full_prefill(gpu):
 
 
 def test_config3_outliers_chunk2048(gpu):
-    """BASELINE config 3 (L=8320, chunk 2048, +-8 outliers in 1% of K): two chunks."""
+    """Config 3 (L=8320, chunk 2048, +-8 outliers in 1% of K): two chunks."""
     k, v, bt = make_cache(8320, 11, std=1.0, outlier_frac=0.01)
     qfull = make_query(8320, 12, std=1.0)
     for c in (prompt_chunks(8320, 2048)[1], prompt_chunks(8320, 2048)[-1]):
