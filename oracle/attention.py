@@ -58,7 +58,9 @@ def online_softmax_weighted_sum(blocks: Iterable[tuple[Sequence[float], Sequence
     """One (max, sum, accumulator) state carried across all blocks.
 
     Masked entries may be given as ``-inf`` or as the finite -3.4028e38 the
-    reference kernel writes (online_softmax.hpp:147); either contributes 0.
+    reference kernel writes (block_epilogue_online_softmax.hpp:147 under
+    operator/op_kernel/vendor/cann_9_0_1/block_sparse_attention/attn_infra/
+    epilogue/block/); either contributes 0.
     """
     m = -math.inf
     l = 0.0

@@ -70,8 +70,10 @@
 // first row, the window bound (with the sink exception on tile 0) on tiles
 // starting below the block's last window start.  Interior tiles run unmasked.
 //
-// Numerics follow the reference order (online_softmax.hpp:1002-1086,
-// rescale_o.hpp:153-344): s*scale -> mask -> row max -> p = exp(s - m) in
+// Numerics follow the reference order (operator/op_kernel/vendor/cann_9_0_1/
+// block_sparse_attention/attn_infra/epilogue/block/
+// block_epilogue_online_softmax.hpp:1002-1086 and
+// block_epilogue_rescale_o.hpp:153-344): s*scale -> mask -> row max -> p = exp(s - m) in
 // fp32 -> P to bf16 (round to nearest even) for PV, row sum from the fp32 p
 // -> O = O*exp(m_old - m_new) + P V -> O / l -> bf16 round to nearest even.
 // Exponentials are exp2 of log2(e)-prescaled scores; split partials merge
