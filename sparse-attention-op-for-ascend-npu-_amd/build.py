@@ -40,6 +40,12 @@ HIP_FLAGS = [
     # Keep MFMA accumulators in VGPRs: the softmax rescales them every tile,
     # and VALU cannot operate on AGPRs without copies.
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # Device code only: no NaN operands, so fmaxf needs no quieting
+    # canonicalisation of its inputs (which doubled the row-max work).  The
+    # kernels never form NaN themselves (masked scores are -inf and an
+    # all-masked row's max is taken as 0).  Host code keeps IEEE NaN
+    # semantics: the C ABI rejects a NaN scale.
+    "-Xarch_device", "-fno-honor-nans",
 ]
 
 

@@ -55,13 +55,15 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
   return TM_OK;
 }
 
-// Split-KV sizing: aim for kTargetItemsPerHead work items per KV head (each
-// item runs as two workgroups, so 32 items per head make two rounds of
-// workgroups over the 256 CUs), and never cut a row block into
-// pieces of fewer than kMinSplitTiles tiles: a split's fp32 partial (66 KB)
-// must stay small next to the K/V it reads (32 KB per tile).
-constexpr int kTargetItemsPerHead = 32;
-constexpr int kMinSplitTiles = 16;
+// Split-KV sizing: cut long row blocks so that the chunk's tiles spread
+// evenly over kTargetItemsPerHead items per KV head -- each item runs as two
+// workgroups of one CU each, so 16 items per head give every one of the 256
+// CUs about the same number of tiles in one round -- and never cut a row block
+// into pieces of fewer than kMinSplitTiles tiles (1024 keys): a split's fp32
+// partial (66 KB) must stay small next to the K/V it reads (16 KB per 32-key
+// tile).  The heaviest items are issued first.
+constexpr int kTargetItemsPerHead = 16;
+constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 
 // Work items per KV head beyond which a launch is refused (its grid would
 // exceed 2^30 workgroups).

@@ -23,21 +23,21 @@ constexpr int kDenseTail = 128;
 constexpr int kSparseBegin = kSinkTokens + kLocalWindow + 1;  // 521
 
 // Kernel tiling.
-constexpr int kKvTile = 64;    // keys per LDS tile (divides the 128-token page)
+constexpr int kKvTile = 32;    // keys per LDS tile (divides the 128-token page)
 constexpr int kRowBlock = 32;  // query tokens per work item
 // One split-KV partial per (KV head, work item), fp32, for each of the 4
 // query heads and 64 lanes: 64 O values, the row max and the lane's partial
 // row sum.
 constexpr int64_t kPartialFloats = int64_t(kGroup) * 64 * (64 + 2);
 constexpr int64_t kPartialBytes = kPartialFloats * 4;
-// Largest number of 64-key tiles one work item may hold: the kernel keeps the
-// item's page numbers in two 64-lane registers.  Longer rows are split.
+// Largest number of tiles one work item may hold: the kernel keeps the item's
+// page numbers in two 64-lane registers.  Longer rows are split.
 constexpr int kMaxItemTiles = 128;
 
 // Largest seq_len / prompt_len the 32-bit position arithmetic accepts.
 constexpr int64_t kMaxPositions = (int64_t(1) << 30);
 
-// Tile schedule of one row block [tb, te): up to two runs of 64-key tiles.
+// Tile schedule of one row block [tb, te): up to two runs of kKvTile-key tiles.
 // A block whose rows are all sparse visits the sink tile plus the tiles of
 // [tb - 512, te); any other block visits [0, te).
 struct TileRuns {
@@ -54,7 +54,7 @@ __host__ __device__ inline TileRuns row_block_tiles(int tb, int te, int sparse_b
   if (local_first <= 0) {
     r.count0 = last + 1;
   } else {
-    r.count0 = 1;  // sink tile [0, 64)
+    r.count0 = 1;  // sink tile [0, kKvTile)
     r.first1 = local_first;
     r.count1 = last - local_first + 1;
   }
@@ -85,7 +85,7 @@ struct KernelParams {
   int sparse_begin;    // 521 for TriangleMix, 0 for dense causal
   int sparse_end;      // max(0, prompt_len-128) for TriangleMix, 0 for dense causal
   int num_row_blocks;
-  int tiles_per_split; // max 64-key tiles per work item
+  int tiles_per_split; // max tiles per work item
   int items_per_head;  // sum over row blocks of their split counts
   int any_split;       // 0: every row block is one item (item index = row-block order)
   float scale_log2;    // softmax scale * log2(e)

@@ -4,21 +4,22 @@
 // ------------------
 // A work item is (row block of 32 query tokens, KV head, KV split); each item
 // runs as two workgroups, one per pair of the KV head's four GQA query heads.
-// A workgroup has four wave64s, one per SIMD: (query head hl of the pair) x
-// (KV half kh).  Wave w owns the 32 rows {32 tokens} x {head 4*kvh + 2*hp +
-// hl} and processes every other tile of the item (even tiles for kh = 0, odd
-// for kh = 1); each K/V tile staged in LDS is read by the two waves of its
-// half, and the two halves merge through LDS at the end.  Splitting the GQA
-// group over two workgroups puts 256 workgroups on the 256 CUs for a
-// 512-token chunk.
+// A workgroup has eight wave64s, two per SIMD: (query head hl of the pair) x
+// (KV quarter kq).  Wave w owns the 32 rows {32 tokens} x {head 4*kvh + 2*hp +
+// hl} and processes every fourth 32-key tile of the item (tiles kq, kq+4,
+// ...); each K/V tile staged in LDS is read by the two waves of its quarter,
+// and the four quarters merge through LDS at the end.  Splitting the GQA group
+// over two workgroups puts 256 workgroups on the 256 CUs for a 512-token
+// chunk; two waves per SIMD let one wave's softmax run while the other's
+// MFMAs occupy the matrix core.
 // The KV tiles of a row block are cut into splits of at most
-// `tiles_per_split` tiles (host-chosen, never below 16 tiles = 1024 keys, so
-// only long dense rows split).  A row block with one split writes its output
-// directly; otherwise every split writes an fp32 partial (O, row max, row
-// sum) to the workspace and a small combine kernel, enqueued right after on
-// the same stream, merges the partials in split order (deterministic) and
-// writes the output.  Chunks without long rows -- every sparse middle chunk --
-// are one launch.
+// `tiles_per_split` tiles (host-chosen: at least 1024 keys, at most
+// kMaxItemTiles tiles), so only long dense rows split.  A row block with one
+// split writes its output directly; otherwise every split writes an fp32
+// partial (O, row max, row sum) to the workspace and a small combine kernel,
+// enqueued right after on the same stream, merges the partials in split order
+// (deterministic) and writes the output.  Chunks without long rows -- every
+// sparse middle chunk -- are one launch.
 // Items are numbered per KV head, heaviest row blocks first; KV head =
 // blockIdx % 8 keeps every workgroup of one KV head on one XCD (workgroups
 // are dispatched round-robin over the 8 XCDs), so both head pairs of a row
@@ -27,38 +28,40 @@
 //
 // Tiles, memory path and pipeline
 // -------------------------------
-// K/V tiles are 64 logical keys aligned to 64, so a tile never straddles a
+// K/V tiles are 32 logical keys aligned to 32, so a tile never straddles a
 // 128-token page: one block-table lookup per tile.  Tiles go from HBM straight
 // into LDS with buffer_load_dwordx4 ... lds (no register staging).  Each wave
-// runs a software pipeline over its tiles: in iteration i it issues the
-// QK^T MFMAs of tile i+1 interleaved with the exponentials of tile i, then the
-// PV MFMAs of tile i interleaved with the mask and row max of tile i+1, so the
-// SIMD's matrix core and VALU work at the same time (one wave per SIMD, the
-// interleave is fixed in program order with scheduling barriers).  LDS holds
-// two K slots and two V slots, each with the tiles of both halves; the DMA of
-// K for iteration i+2 and of V for iteration i+1 is issued right after the
-// barrier that opens iteration i.  The four slots are distinct LDS objects
-// and the loop is unrolled by two so every access names its slot statically:
-// the compiler then sees that the prefetch never aliases the tiles being
-// read and does not wait for it.  Each tile is addressed through a buffer
-// resource whose range stops at seq_len, so key rows past seq_len read as
-// zeros.  LDS rows are 256 B (one key x 128 dims) with the 16-byte chunks
-// XOR-swizzled so both read patterns are bank-conflict free:
+// runs a software pipeline over its tiles: in iteration i it issues the QK^T
+// MFMAs of its tile of iteration i+1 interleaved with the exponentials of its
+// tile of iteration i, then the PV MFMAs of tile i interleaved with the mask
+// and row max of tile i+1 (the interleave is fixed in program order with
+// scheduling barriers).  LDS holds two K slots and two V slots, each with the
+// four tiles (one per quarter) of one iteration; the DMA of K for iteration
+// i+2 (waves 0-3) and of V for iteration i+1 (waves 4-7) is spread over the
+// MFMA steps of iteration i, one instruction per step.  The four slots are
+// distinct LDS objects and the loop is unrolled by two so every access names
+// its slot statically: the compiler then sees that the prefetch never aliases
+// the tiles being read and does not wait for it.  Each wave waits for its own
+// DMA (vmcnt 0) before the barrier that opens the next iteration.  Each tile
+// is addressed through a buffer resource whose range stops at seq_len, so key
+// rows past seq_len read as zeros.  LDS rows are 256 B (one key x 128 dims)
+// with the 16-byte chunks XOR-swizzled so both read patterns are bank-conflict
+// free:
 //   K: chunk c of key row r sits in slot c ^ (r % 16)
 //   V: chunk c of key row r sits in slot c ^ (4 * (r % 4))
 //
 // Contractions (per wave, v_mfma_f32_32x32x16_bf16)
 // ---------------------------------------------------
-//   S^T (64 keys x 32 rows) = K Q^T   A = K rows from LDS, B = Q in registers
+//   S^T (32 keys x 32 rows) = K Q^T   A = K rows from LDS, B = Q in registers
 //   O^T (128 x 32 rows)    += V^T P^T  A = V via ds_read_b64_tr_b16, B = P
 // In the 32x32 accumulator layout lane l owns column l % 32, i.e. one query
-// row: accumulator element v of key block b is key 32b + 8(v/4) + 4(l/32) +
-// v%4.  Row max / row sum are lane-local plus one exchange between the two
-// 32-lane halves, and the fp32 scores convert in registers into the bf16 B
-// operand of PV.  ds_read_b64_tr_b16 transposes within 16-lane groups: when
-// the 4 source lanes 4j..4j+3 of a group point at 4 consecutive dims of key
-// row j, destination lane t of the group receives dim t of keys 0..3 --
-// exactly the A-operand slice (one dim, four consecutive keys) of V^T.
+// row: accumulator element v is key 8(v/4) + 4(l/32) + v%4 of the tile.  Row
+// max / row sum are lane-local plus one exchange between the two 32-lane
+// halves (v_permlane32_swap), and the fp32 scores convert in registers into
+// the bf16 B operand of PV.  ds_read_b64_tr_b16 transposes within 16-lane
+// groups: when the 4 source lanes 4j..4j+3 of a group point at 4 consecutive
+// dims of key row j, destination lane t of the group receives dim t of keys
+// 0..3 -- exactly the A-operand slice (one dim, four consecutive keys) of V^T.
 //
 // Mask
 // ----
@@ -76,8 +79,8 @@
 // block_epilogue_rescale_o.hpp:153-344): s*scale -> mask -> row max -> p = exp(s - m) in
 // fp32 -> P to bf16 (round to nearest even) for PV, row sum from the fp32 p
 // -> O = O*exp(m_old - m_new) + P V -> O / l -> bf16 round to nearest even.
-// Exponentials are exp2 of log2(e)-prescaled scores; split partials merge
-// with the same rescale rule.
+// Exponentials are exp2 of log2(e)-prescaled scores; the KV quarters and the
+// split partials merge with the same rescale rule.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -94,19 +97,24 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 #define TM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-constexpr int kWaves = 4;                        // 2 query heads x 2 KV halves
-constexpr int kThreads = kWaves * 64;
 constexpr int kHeadsPerGroup = 2;                // query heads per workgroup
+constexpr int kQuarters = 4;                     // KV quarters per workgroup
+constexpr int kWaves = kHeadsPerGroup * kQuarters;
+constexpr int kThreads = kWaves * 64;
 constexpr int kGroupsPerKvHead = kGroup / kHeadsPerGroup;
 constexpr int kRowBytes = kHeadDim * 2;          // 256 B: one key row
-constexpr int kTileBytes = kKvTile * kRowBytes;  // 16 KB: K or V of one tile
-constexpr int kSlotBytes = 2 * kTileBytes;       // the tiles of both KV halves of one iteration
+constexpr int kTileBytes = kKvTile * kRowBytes;  // 8 KB: K or V of one tile
+constexpr int kSlotBytes = kQuarters * kTileBytes;  // the tiles of all quarters of one iteration
+constexpr int kDmaPerTile = kTileBytes / 1024;   // 1 KB (4 key rows) per DMA instruction
 // Buffer-resource word 3 for raw (unformatted, stride 0) dword loads on gfx9.
 constexpr int kBufferFlags = 0x00020000;
+// A buffer offset past every range used here: such a load returns 0.
+constexpr unsigned kOutOfRange = 0x40000000u;
 
-static_assert(kKvTile == 64 && kPageSize % kKvTile == 0, "a tile must stay inside one page");
+static_assert(kKvTile == 32 && kPageSize % kKvTile == 0, "a tile must stay inside one page");
 static_assert(kRowBlock == 32, "one MFMA column per query token");
-static_assert(kWaves * 16 == kKvTile, "each wave loads 16 key rows of every tile");
+static_assert(kWaves == 2 * kQuarters && kDmaPerTile == 8,
+              "each wave loads one tile per iteration, one DMA instruction per MFMA step");
 
 // Wait until every LDS DMA (and other vector-memory load) this wave issued has
 // landed: s_waitcnt vmcnt(0), expcnt / lgkmcnt unconstrained.  Each wave runs
@@ -166,48 +174,44 @@ __device__ __forceinline__ float other_half(float x) {
   return __uint_as_float(__lane_id() < 32 ? r[1] : r[0]);
 }
 
-// Key offset inside the tile of accumulator element v of key block b, for
-// lanes of the first 32-lane half (the second half adds 4).
-__device__ __forceinline__ constexpr int elem_key(int b, int v) { return 32 * b + 8 * (v >> 2) + (v & 3); }
+// Key offset inside the tile of accumulator element v, for lanes of the
+// first 32-lane half (the second half adds 4).
+__device__ __forceinline__ constexpr int elem_key(int v) { return 8 * (v >> 2) + (v & 3); }
 
-// MFMA step k of S^T = K Q^T (k = 0..15: key block b = k % 2, dims
-// 16c .. 16c+15 with c = k / 2): the K operand read from LDS.
-__device__ __forceinline__ bf16x8_t k_operand(const char* kt, const int* k_off, int k) {
-  return *reinterpret_cast<const bf16x8_t*>(kt + 32 * (k & 1) * kRowBytes + k_off[k >> 1]);
+// MFMA step c of S^T = K Q^T (dims 16c .. 16c+15): the K operand from LDS.
+__device__ __forceinline__ bf16x8_t k_operand(const char* kt, const int* k_off, int c) {
+  return *reinterpret_cast<const bf16x8_t*>(kt + k_off[c]);
 }
 
-// S^T = K Q^T for one 64-key tile (raw scores, two 32-key blocks).
-__device__ __forceinline__ void qk_tile(const char* kt, const int* k_off, const bf16x8_t* qreg, f32x16_t* s) {
-  bf16x8_t kf[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) kf[k] = k_operand(kt, k_off, k);
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int b = k & 1, c = k >> 1;
-    s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qreg[c], c == 0 ? f32x16_t{} : s[b], 0, 0, 0);
-  }
+// MFMA step k of O^T += V^T P^T (k = 0..7: d-block m = k % 4, k-group j = k / 4
+// of 16 keys): the V^T operand, two transposed reads.  k-slot e of half h in
+// k-group j is key 16j + 8(e/4) + 4h + e%4 -- the keys of P's bf16 lane
+// vector pb[j].
+__device__ __forceinline__ bf16x8_t v_operand(const char* vt, const int* v_off, int k) {
+  const char* a0 = vt + 16 * (k >> 2) * kRowBytes + v_off[k & 3];
+  const i16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(a0));
+  const i16x4_t hi4 =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(a0 + 8 * kRowBytes));
+  const i16x4_t lohi[2] = {lo4, hi4};
+  bf16x8_t a;
+  __builtin_memcpy(&a, lohi, sizeof(a));
+  return a;
 }
+
+// How many MFMA steps ahead of their use the LDS operand reads are issued.
+constexpr int kReadAhead = 3;
 
 // Causal bound: keep elements whose key offset is <= thr (per lane).
-__device__ __forceinline__ void mask_causal(f32x16_t* s, int thr) {
+__device__ __forceinline__ void mask_causal(f32x16_t& s, int thr) {
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) s[b][v] = elem_key(b, v) <= thr ? s[b][v] : -INFINITY;
-  }
+  for (int v = 0; v < 16; ++v) s[v] = elem_key(v) <= thr ? s[v] : -INFINITY;
 }
 
 // Window bound: keep elements whose key offset is >= thr; the elements that
-// can hold sink keys (b = 0, v < 4) compare against thr_sink instead.
-__device__ __forceinline__ void mask_window(f32x16_t* s, int thr, int thr_sink) {
+// can hold sink keys (v < 4 on tile 0) compare against thr_sink instead.
+__device__ __forceinline__ void mask_window(f32x16_t& s, int thr, int thr_sink) {
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int t = (b == 0 && v < 4) ? thr_sink : thr;
-      s[b][v] = elem_key(b, v) >= t ? s[b][v] : -INFINITY;
-    }
-  }
+  for (int v = 0; v < 16; ++v) s[v] = elem_key(v) >= (v < 4 ? thr_sink : thr) ? s[v] : -INFINITY;
 }
 
 // Online softmax of one tile in the log2 domain (max commutes with the
@@ -229,27 +233,10 @@ __device__ __forceinline__ float softmax_update(float m_tile, float& m_run, floa
   return m_run == -INFINITY ? 0.0f : m_run;
 }
 
-// MFMA step k of O^T += V^T P^T (k = 0..15: d-block m = k % 4, k-group
-// bj = k / 4 = 2b + j of 16 keys): the V^T operand, two transposed reads.
-// k-slot e of half h in k-group (b, j) is key 32b + 16j + 8(e/4) + 4h + e%4.
-__device__ __forceinline__ bf16x8_t v_operand(const char* vt, const int* v_off, int k) {
-  const char* a0 = vt + 16 * (k >> 2) * kRowBytes + v_off[k & 3];
-  const i16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(a0));
-  const i16x4_t hi4 =
-      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(a0 + 8 * kRowBytes));
-  const i16x4_t lohi[2] = {lo4, hi4};
-  bf16x8_t a;
-  __builtin_memcpy(&a, lohi, sizeof(a));
-  return a;
-}
-
-// How many MFMA steps ahead of their use the LDS operand reads are issued.
-constexpr int kReadAhead = 4;
-
 template <bool kSparse>
 __global__ void __launch_bounds__(kThreads)
 triangle_paged_attention_kernel(KernelParams p) {
-  // K slots 0/1 and V slots 0/1: tiles of iteration i live in slot i % 2.
+  // K slots 0/1 and V slots 0/1: the four tiles of iteration i live in slot i % 2.
   __shared__ __attribute__((aligned(1024))) char k_lds0[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) char k_lds1[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) char v_lds0[kSlotBytes];
@@ -258,7 +245,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, kept scalar
   const int hl = wave & 1;   // query head inside the workgroup's pair
-  const int kh = wave >> 1;  // KV half: even (0) or odd (1) tiles of the item
+  const int kq = wave >> 1;  // KV quarter: tiles kq, kq+4, ... of the item
   const int lane = tid & 63;
   const int n = lane & 31;  // MFMA column = query token of this lane
   const int half = lane >> 5;
@@ -292,40 +279,72 @@ triangle_paged_attention_kernel(KernelParams p) {
 
   const TileRuns runs = row_block_tiles(tb, te, sparse_begin, sparse_end);
   const int all_tiles = runs.count();
-  const int t_lo = (int)((long long)split * all_tiles / nsplit);
-  const int t_hi = (int)((long long)(split + 1) * all_tiles / nsplit);
-  const int num_tiles = t_hi - t_lo;
-  const int num_iters = (num_tiles + 1) >> 1;
+  // Split s of n takes tiles [s*b + min(s, r), ...) with b = all / n and
+  // r = all % n: the first r splits get b + 1 tiles, the rest b.
+  int t_lo = 0;
+  int num_tiles = all_tiles;
+  if (p.any_split) {
+    const int base = all_tiles / nsplit;
+    const int rem = all_tiles - base * nsplit;
+    t_lo = split * base + min(split, rem);
+    num_tiles = base + (split < rem ? 1 : 0);
+  }
+  const int num_iters = (num_tiles + kQuarters - 1) / kQuarters;
 
-  // ---- DMA: wave w loads key rows 16w .. 16w+15 of every tile ----
-  // Four wave-instructions of 1 KB (4 key rows) per tile and tensor.  Lane i
-  // writes LDS slot (row 16w + 4j + i/16, slot i%16), so it loads the global
-  // chunk the swizzle puts in that slot.
-  const int dma_slot = lane & 15;
-  unsigned dma_voff[2][4];
+  // ---- DMA: per iteration, wave w loads one whole tile ----
+  // Waves 0-3 load the K tile of quarter w, waves 4-7 the V tile of quarter
+  // w - 4: eight wave-instructions of 1 KB (4 key rows).  Lane i of
+  // instruction j writes LDS slot (row 4j + i/16, slot i%16), so it loads the
+  // global chunk the swizzle puts in that slot.
+  const int dma_t = wave >> 2;  // 0 = K, 1 = V
+  const int dma_u = wave & 3;   // quarter
+  unsigned dma_voff[kDmaPerTile];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = 16 * wave + 4 * j + (lane >> 4);
-    dma_voff[0][j] = (unsigned)(row * kKvHeads * kRowBytes + 16 * k_slot(row, dma_slot));
-    dma_voff[1][j] = (unsigned)(row * kKvHeads * kRowBytes + 16 * v_slot(row, dma_slot));
+  for (int j = 0; j < kDmaPerTile; ++j) {
+    const int row = 4 * j + (lane >> 4);
+    const int slot = dma_t == 0 ? k_slot(row, lane & 15) : v_slot(row, lane & 15);
+    dma_voff[j] = (unsigned)(row * kKvHeads * kRowBytes + 16 * slot);
   }
   // Physical page of every tile of the item (at most kMaxItemTiles = 128):
-  // lane i of page_lo / page_hi holds tile i / 64 + i (one vector load each,
-  // issued with the Q loads); the loop reads them with v_readlane, so it never
-  // waits on a scalar memory load (whose counter it shares with the LDS reads).
+  // lane i of page_lo / page_hi holds tile i / 64 + i; the loop reads them
+  // with v_readlane, so it never waits on a scalar memory load (whose counter
+  // it shares with the LDS reads).  Both these loads and the Q loads below go
+  // through buffer resources whose range ends at the data: an offset past it
+  // reads 0, so no load sits in a divergent branch (the compiler waits for a
+  // load before such a branch joins, which would serialise the round trips).
+  // Order: block table first, then Q, then the tile DMA -- loads complete in
+  // issue order, so the DMA (which needs the page numbers) does not wait for
+  // Q, and Q's latency hides behind the block-table round trip.
+  const int logical_pages = (p.seq_len + kPageSize - 1) / kPageSize;
+  const __amdgpu_buffer_rsrc_t bt_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.block_table, (short)0, logical_pages * 4, kBufferFlags);
   auto lane_page = [&](int ti) {
-    int phys = 0;
-    if (ti < num_tiles) phys = p.block_table[runs.tile(t_lo + ti) * kKvTile / kPageSize];
+    const unsigned off = ti < num_tiles ? (unsigned)(runs.tile(t_lo + ti) * kKvTile / kPageSize) * 4u : kOutOfRange;
+    const int phys = __builtin_amdgcn_raw_buffer_load_b32(bt_rsrc, off, 0, 0);
     return min(max(phys, 0), p.num_pages - 1);
   };
   const int page_lo = lane_page(lane);
   const int page_hi = lane_page(64 + lane);
+  // ---- Q^T operand: lane (token n, half) holds Q[q][head][16c + 8*half .. +8] ----
+  // The range is the row block's rows: rows past seq_len read 0.
+  bf16x8_t qreg[kHeadDim / 16];
+  {
+    const __amdgpu_buffer_rsrc_t q_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.query + (size_t)(tb - p.query_start) * kQueryHeads * kHeadDim), (short)0,
+        (te - tb) * kQueryHeads * kHeadDim * 2, kBufferFlags);
+    const unsigned qoff = (unsigned)(((n * kQueryHeads + head) * kHeadDim + 8 * half) * 2);
+#pragma unroll
+    for (int c = 0; c < kHeadDim / 16; ++c) {
+      qreg[c] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, qoff + 32 * c, 0, 0));
+    }
+  }
+
   auto tile_page = [&](int ti) {
     return __builtin_amdgcn_readlane(ti < 64 ? page_lo : page_hi, ti & 63);
   };
-  // Buffer resource of tensor t (0 = K, 1 = V) of tile ti: the tile's 64 key
-  // rows of this KV head, range cut at seq_len; a tile past the item's end
-  // gets an empty range (its loads return zeros).
+  // Buffer resource of tensor t (0 = K, 1 = V) of tile ti: the tile's key rows
+  // of this KV head, range cut at seq_len; a tile past the item's end gets an
+  // empty range (its loads return zeros).
   auto tile_rsrc = [&](int ti, int t) {
     const bool live = ti < num_tiles;
     const int phys = tile_page(ti);
@@ -336,37 +355,22 @@ triangle_paged_attention_kernel(KernelParams p) {
     const __bf16* cache = t == 0 ? p.key_cache : p.value_cache;
     return __builtin_amdgcn_make_buffer_rsrc((void*)(cache + first_row), (short)0, bytes, kBufferFlags);
   };
-  // DMA instruction j (0..3) of this wave for one tile: 4 key rows.
-  auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int t, char* lds_tile, int j) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TM_LDS(lds_tile + (4 * wave + j) * 1024), 16, dma_voff[t][j], 0, 0,
-                                             0);
+  // DMA instruction j of this wave's tile of one iteration.
+  auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, char* lds_tile, int j) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TM_LDS(lds_tile + j * 1024), 16, dma_voff[j], 0, 0, 0);
   };
   auto issue_tile = [&](int ti, int t, char* lds_tile) {
     const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(ti, t);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma(rsrc, t, lds_tile, j);
+    for (int j = 0; j < kDmaPerTile; ++j) dma(rsrc, lds_tile, j);
   };
 
   // Prologue DMA: K and V of iteration 0, K of iteration 1.
-  if (num_iters > 0) {
-    issue_tile(0, 0, k_lds0);
-    issue_tile(1, 0, k_lds0 + kTileBytes);
-    issue_tile(0, 1, v_lds0);
-    issue_tile(1, 1, v_lds0 + kTileBytes);
-  }
-  if (num_iters > 1) {
-    issue_tile(2, 0, k_lds1);
-    issue_tile(3, 0, k_lds1 + kTileBytes);
-  }
-
-  // ---- Q^T operand: lane (token n, half) holds Q[q][head][16c + 8*half .. +8] ----
-  bf16x8_t qreg[kHeadDim / 16];
-  {
-    const __bf16* qrow = p.query + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim + 8 * half;
-#pragma unroll
-    for (int c = 0; c < kHeadDim / 16; ++c) {
-      qreg[c] = row_active ? *reinterpret_cast<const bf16x8_t*>(qrow + 16 * c) : bf16x8_t{};
-    }
+  if (dma_t == 0) {
+    issue_tile(dma_u, 0, k_lds0 + dma_u * kTileBytes);
+    issue_tile(kQuarters + dma_u, 0, k_lds1 + dma_u * kTileBytes);
+  } else {
+    issue_tile(dma_u, 1, v_lds0 + dma_u * kTileBytes);
   }
 
   // ---- mask geometry ----
@@ -389,15 +393,14 @@ triangle_paged_attention_kernel(KernelParams p) {
 #pragma unroll
   for (int m = 0; m < kHeadDim / 32; ++m) o_acc[m] = f32x16_t{};
 
-  // Per-lane LDS read offsets inside a 16 KB tile (loop invariant).
-  // K (A operand of QK): row 32b + n, chunk 2c + half; the swizzle depends on
-  // row % 16 = n % 16 only, so b adds the constant 32 rows.
+  // Per-lane LDS read offsets inside a tile (loop invariant).
+  // K (A operand of QK): row n, chunk 2c + half.
   int k_off[kHeadDim / 16];
 #pragma unroll
   for (int c = 0; c < kHeadDim / 16; ++c) k_off[c] = n * kRowBytes + 16 * k_slot(n, 2 * c + half);
   // V (A operand of PV, transposed read): 16-lane group g = lane/16 reads key
   // quad 4*(g/2) + (lane%16)/4 at dims 32m + 16*(g%2) + 4*(lane%4); the key
-  // offsets kb and +8 are multiples of 4, so they do not change the swizzle.
+  // offsets 16j and +8 are multiples of 4, so they do not change the swizzle.
   const int tr_key = 4 * (lane >> 5) + ((lane & 15) >> 2);
   int v_off[kHeadDim / 32];
 #pragma unroll
@@ -406,13 +409,12 @@ triangle_paged_attention_kernel(KernelParams p) {
     v_off[m] = tr_key * kRowBytes + 16 * v_slot(tr_key, d >> 3) + 2 * (d & 7);
   }
   const float c2 = p.scale_log2;
-  const int tile_off = kh * kTileBytes;  // this wave's tile inside a slot
+  const int tile_off = kq * kTileBytes;    // this wave's tile inside a slot
+  const int dma_off = dma_u * kTileBytes;  // the tile this wave loads
 
-  wait_dma();
-  __syncthreads();  // prologue DMA of every wave landed
-  // Mask of tile ti of this wave (in place, before its row max), applied only
+  // Mask of tile ti of the item (in place, before its row max), applied only
   // where some (row, key) pair of the tile is outside the row's keys.
-  auto mask_tile = [&](f32x16_t* s, int ti) {
+  auto mask_tile = [&](f32x16_t& s, int ti) {
     const int k0 = runs.tile(t_lo + min(ti, num_tiles - 1)) * kKvTile;
     if (k0 + kKvTile - 1 > tb) mask_causal(s, q_rel - k0);
     if (kSparse && k0 < lo_max) {
@@ -421,45 +423,44 @@ triangle_paged_attention_kernel(KernelParams p) {
     }
   };
 
-  f32x16_t s_a[2], s_b[2];
+  wait_dma();
+  __syncthreads();  // prologue DMA of every wave landed
+  f32x16_t s_a, s_b;
   float m_tile = -INFINITY;  // row max of the tile the next iteration exponentiates (log2 units)
-  if (kh < num_tiles) {
-    qk_tile(k_lds0 + tile_off, k_off, qreg, s_a);
-    mask_tile(s_a, kh);
+  if (kq < num_tiles) {
+    s_a = f32x16_t{};
+#pragma unroll
+    for (int c = 0; c < kHeadDim / 16; ++c) {
+      s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_operand(k_lds0 + tile_off, k_off, c), qreg[c], s_a, 0, 0, 0);
+    }
+    mask_tile(s_a, kq);
     float tmax = -INFINITY;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) tmax = fmaxf(tmax, s_a[b][v]);
-    }
+    for (int v = 0; v < 16; ++v) tmax = fmaxf(tmax, s_a[v]);
     m_tile = fmaxf(tmax, other_half(tmax)) * c2;
   }
 
-  // Iteration it (this wave's tile ti = 2*it + kh): state update with tile
-  // ti's row max, then [QK^T of tile ti+2 (K slot kr) || exponentials of tile
-  // ti], then [PV of tile ti (V slot vr) || mask and row max of tile ti+2];
-  // the prefetch of K for iteration it+2 into kw and V for it+1 into vw is
-  // spread over the first block.
-  auto iteration = [&](int it, f32x16_t* s_cur, f32x16_t* s_nxt, const char* kr, const char* vr, char* kw,
+  // Iteration it (this wave's tile ti = 4*it + kq): state update with tile
+  // ti's row max, then [QK^T of tile ti+4 (K slot kr) || exponentials of tile
+  // ti], then [PV of tile ti (V slot vr) || mask and row max of tile ti+4];
+  // the prefetch of K for iteration it+2 into kw and V for it+1 into vw (one
+  // tile per wave) is spread over the first block.
+  auto iteration = [&](int it, f32x16_t& s_cur, f32x16_t& s_nxt, const char* kr, const char* vr, char* kw,
                        char* vw) {
     wait_dma();
     __syncthreads();  // DMA issued one iteration ago landed; slots kw / vw are no longer read
-    const int ti = 2 * it + kh;
-    // Odd tile count: half 1 idles in the last iteration, which prefetches nothing.
+    const int ti = kQuarters * it + kq;
+    // Ragged last iteration: the quarters without a tile idle; nothing is
+    // left to prefetch in the last iteration.
     if (ti >= num_tiles) return;
-    // This iteration's prefetch -- K of iteration it+2 into kw, V of it+1 into
-    // vw -- goes out one DMA instruction per MFMA step below, so its issue
-    // overlaps the MFMAs instead of stalling the wave in one burst.
-    // Past the item's last iteration the resources are empty: those loads
-    // return zeros into a slot nobody reads, which keeps the steps below
-    // free of branches (a branch would let the compiler move the softmax work
-    // out of the MFMA steps).
-    __amdgpu_buffer_rsrc_t dma_rsrc[2][2];  // [tensor][tile of the pair]
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      dma_rsrc[0][u] = tile_rsrc(it + 2 < num_iters ? 2 * (it + 2) + u : num_tiles, 0);
-      dma_rsrc[1][u] = tile_rsrc(it + 1 < num_iters ? 2 * (it + 1) + u : num_tiles, 1);
-    }
+    // This wave's prefetch: K of iteration it+2 (waves 0-3) or V of it+1
+    // (waves 4-7).  Past the item's last iteration the resource is empty:
+    // those loads return zeros into a slot nobody reads, which keeps the steps
+    // below free of branches.
+    const int pf_it = dma_t == 0 ? it + 2 : it + 1;
+    const __amdgpu_buffer_rsrc_t pf_rsrc =
+        tile_rsrc(pf_it < num_iters ? kQuarters * pf_it + dma_u : num_tiles, dma_t);
+    char* pf_lds = (dma_t == 0 ? kw : vw) + dma_off;
     const float shift = softmax_update(m_tile, m_run, l_run, o_acc);
     // Block 1: the QK^T MFMAs of the next tile (run unconditionally: past the
     // last tile they read a stale slot and the result is unused) interleaved,
@@ -469,44 +470,42 @@ triangle_paged_attention_kernel(KernelParams p) {
     // their MFMA; the last steps also start the V reads of block 2.
     const char* kt = kr + tile_off;
     const char* vt = vr + tile_off;
-    bf16x8_t kf[16], va[16];
+    bf16x8_t kf[8], va[8];
 #pragma unroll
     for (int k = 0; k < kReadAhead; ++k) kf[k] = k_operand(kt, k_off, k);
-    bf16x8_t pb[2][2];
+    bf16x8_t pb[2];
     float rsum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      dma(dma_rsrc[k >> 3][(k >> 2) & 1], k >> 3, ((k >> 3) == 0 ? kw : vw) + ((k >> 2) & 1) * kTileBytes, k & 3);
-      if (k + kReadAhead < 16) {
+    for (int k = 0; k < 8; ++k) {
+      dma(pf_rsrc, pf_lds, k);
+      if (k + kReadAhead < 8) {
         kf[k + kReadAhead] = k_operand(kt, k_off, k + kReadAhead);
       } else {
-        va[k + kReadAhead - 16] = v_operand(vt, v_off, k + kReadAhead - 16);
+        va[k + kReadAhead - 8] = v_operand(vt, v_off, k + kReadAhead - 8);
       }
-      const int b = k & 1, c = k >> 1;
-      s_nxt[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qreg[c], c == 0 ? f32x16_t{} : s_nxt[b], 0, 0, 0);
+      s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qreg[k], k == 0 ? f32x16_t{} : s_nxt, 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const int e = 2 * k + t, eb = e >> 4, ev = e & 15;
-        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[eb][ev], c2, -shift));
+        const int e = 2 * k + t;
+        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[e], c2, -shift));
         rsum += x;
-        pb[eb][ev >> 3][ev & 7] = (__bf16)x;
+        pb[e >> 3][e & 7] = (__bf16)x;
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     l_run += rsum;
     // An empty statement that consumes P here keeps the exponentials in block
     // 1 (otherwise they sink past the mask branches below, next to their use).
-    asm volatile("" ::"v"(pb[0][0]), "v"(pb[0][1]), "v"(pb[1][0]), "v"(pb[1][1]), "v"(l_run));
+    asm volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(l_run));
     // Block 2: the PV MFMAs of this tile interleaved with the row max of the
     // next one (masked first; its state update opens the next iteration).
-    mask_tile(s_nxt, ti + 2);
+    mask_tile(s_nxt, ti + kQuarters);
     float tmax = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      if (k + kReadAhead < 16) va[k + kReadAhead] = v_operand(vt, v_off, k + kReadAhead);
-      const int bj = k >> 2;
-      o_acc[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[k], pb[bj >> 1][bj & 1], o_acc[k & 3], 0, 0, 0);
-      tmax = fmaxf(tmax, fmaxf(s_nxt[k >> 3][(2 * k) & 15], s_nxt[k >> 3][(2 * k + 1) & 15]));
+    for (int k = 0; k < 8; ++k) {
+      if (k + kReadAhead < 8) va[k + kReadAhead] = v_operand(vt, v_off, k + kReadAhead);
+      o_acc[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[k], pb[k >> 2], o_acc[k & 3], 0, 0, 0);
+      tmax = fmaxf(tmax, fmaxf(s_nxt[2 * k], s_nxt[2 * k + 1]));
       __builtin_amdgcn_sched_barrier(0);
     }
     m_tile = fmaxf(tmax, other_half(tmax)) * c2;
@@ -516,44 +515,58 @@ triangle_paged_attention_kernel(KernelParams p) {
     if (it + 1 < num_iters) iteration(it + 1, s_b, s_a, k_lds0, v_lds1, k_lds1, v_lds0);
   }
 
-  // ---- merge the two KV halves through LDS ----
-  // Half kh keeps d-blocks 2*kh, 2*kh+1 and hands the other two to its partner.
+  // ---- merge the four KV quarters through LDS ----
+  // Quarter kq keeps d-block kq and hands its three other d-blocks to their
+  // owners.  Given block index gi (0..2 among the blocks a quarter gives away)
+  // selects the slot: xo_gi[hl][quarter][v][lane] lives in k_lds0, k_lds1,
+  // v_lds0 for gi = 0, 1, 2; xm / xl [hl][quarter][lane] live in v_lds1.
   wait_dma();
   __syncthreads();  // all compute and every (empty) prefetch done; the slots are free
-  float* xo = reinterpret_cast<float*>(k_lds0);  // [kh][hl][2 blocks][v][lane]
-  static_assert(2 * kHeadsPerGroup * 2 * 16 * 64 * 4 == kSlotBytes, "exchanged O fills one slot");
-  float* xm = reinterpret_cast<float*>(v_lds0);  // [kh][hl][lane]
-  float* xl = xm + 2 * kHeadsPerGroup * 64;
-  const int keep = 2 * kh;
-  f32x16_t kept[2], given[2];
-  if (kh == 0) {
-    kept[0] = o_acc[0]; kept[1] = o_acc[1]; given[0] = o_acc[2]; given[1] = o_acc[3];
-  } else {
-    kept[0] = o_acc[2]; kept[1] = o_acc[3]; given[0] = o_acc[0]; given[1] = o_acc[1];
-  }
-  const int self = kh * kHeadsPerGroup + hl;
+  static_assert(kHeadsPerGroup * kQuarters * 16 * 64 * 4 == kSlotBytes, "one given block fills one slot");
+  auto xo = [&](int gi) {
+    return reinterpret_cast<float*>(gi == 0 ? k_lds0 : (gi == 1 ? k_lds1 : v_lds0));
+  };
+  float* xm = reinterpret_cast<float*>(v_lds1);
+  float* xl = xm + kHeadsPerGroup * kQuarters * 64;
+  const int self = hl * kQuarters + kq;
 #pragma unroll
-  for (int mm = 0; mm < 2; ++mm) {
+  for (int m = 0; m < kHeadDim / 32; ++m) {
+    if (m == kq) continue;
+    const int gi = m < kq ? m : m - 1;  // index of block m among those this quarter gives away
+    float* dst = xo(gi) + self * 16 * 64 + lane;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) xo[((self * 2 + mm) * 16 + v) * 64 + lane] = given[mm][v];
+    for (int v = 0; v < 16; ++v) dst[v * 64] = o_acc[m][v];
   }
   xm[self * 64 + lane] = m_run;
   xl[self * 64 + lane] = l_run;
   __syncthreads();
-  const int other = (kh ^ 1) * kHeadsPerGroup + hl;
+  f32x16_t kept = o_acc[0];
+#pragma unroll
+  for (int m = 1; m < kHeadDim / 32; ++m) kept = m == kq ? o_acc[m] : kept;
   {
-    const float m1 = xm[other * 64 + lane];
-    const float l1 = xl[other * 64 + lane];
-    const float mt = fmaxf(m_run, m1);
-    const float mu = mt == -INFINITY ? 0.0f : mt;
-    const float a0 = __builtin_amdgcn_exp2f(m_run - mu);
-    const float a1 = __builtin_amdgcn_exp2f(m1 - mu);
-    l_run = l_run * a0 + l1 * a1;
+    float mq[kQuarters], lq[kQuarters];
+    float mt = -INFINITY;
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) kept[mm][v] = kept[mm][v] * a0 + xo[((other * 2 + mm) * 16 + v) * 64 + lane] * a1;
+    for (int r = 0; r < kQuarters; ++r) {
+      mq[r] = xm[(hl * kQuarters + r) * 64 + lane];
+      lq[r] = xl[(hl * kQuarters + r) * 64 + lane];
+      mt = fmaxf(mt, mq[r]);
     }
+    const float mu = mt == -INFINITY ? 0.0f : mt;
+    float lt = 0.0f;
+    f32x16_t acc = kept * __builtin_amdgcn_exp2f(m_run - mu);
+#pragma unroll
+    for (int r = 0; r < kQuarters; ++r) {
+      const float a = __builtin_amdgcn_exp2f(mq[r] - mu);
+      lt += lq[r] * a;
+      if (r == kq) continue;
+      const int gi = kq < r ? kq : kq - 1;  // index of block kq among those quarter r gives away
+      const float* src = xo(gi) + (hl * kQuarters + r) * 16 * 64 + lane;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[v] += src[v * 64] * a;
+    }
+    kept = acc;
+    l_run = lt;
     m_run = mt;
   }
 
@@ -563,14 +576,11 @@ triangle_paged_attention_kernel(KernelParams p) {
     if (!row_active) return;
     __bf16* orow = p.out + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim;
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
+    for (int g = 0; g < 4; ++g) {
+      bf16x4_t o4;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        bf16x4_t o4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(kept[mm][4 * g + e] * inv);
-        *reinterpret_cast<bf16x4_t*>(orow + 32 * (keep + mm) + 8 * g + 4 * half) = o4;
-      }
+      for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(kept[4 * g + e] * inv);
+      *reinterpret_cast<bf16x4_t*>(orow + 32 * kq + 8 * g + 4 * half) = o4;
     }
     return;
   }
@@ -579,17 +589,14 @@ triangle_paged_attention_kernel(KernelParams p) {
   // Layout per (KV head, item): O [hq][m][v/4][lane][v%4], then row max
   // [hq][lane], then the lane's partial row sum [hq][lane] -- every access is
   // a lane-contiguous 16- or 4-byte vector.  The two head-pair workgroups
-  // write disjoint heads.
+  // write disjoint heads, the four quarters disjoint d-blocks.
   float* part = p.partials + ((size_t)kvh * p.items_per_head + item) * kPartialFloats;
 #pragma unroll
-  for (int mm = 0; mm < 2; ++mm) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4_t o4 = {kept[mm][4 * g], kept[mm][4 * g + 1], kept[mm][4 * g + 2], kept[mm][4 * g + 3]};
-      *reinterpret_cast<f32x4_t*>(part + (((hq * 4 + keep + mm) * 4 + g) * 64 + lane) * 4) = o4;
-    }
+  for (int g = 0; g < 4; ++g) {
+    const f32x4_t o4 = {kept[4 * g], kept[4 * g + 1], kept[4 * g + 2], kept[4 * g + 3]};
+    *reinterpret_cast<f32x4_t*>(part + (((hq * 4 + kq) * 4 + g) * 64 + lane) * 4) = o4;
   }
-  if (kh == 0) {  // both halves hold the same merged row max and row sum
+  if (kq == 0) {  // every quarter holds the same merged row max and row sum
     part[kGroup * 64 * 64 + hq * 64 + lane] = m_run;
     part[kGroup * 64 * 65 + hq * 64 + lane] = l_run;
   }

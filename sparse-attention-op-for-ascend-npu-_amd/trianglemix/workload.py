@@ -94,12 +94,12 @@ def kv_bytes(c: Chunk, *, dense: bool = False) -> int:
     return unique_kv_tokens(c, dense=dense) * HKV * D * 2 * 2
 
 
-KV_TILE = 64   # keys per kernel tile
+KV_TILE = 32   # keys per kernel tile
 ROW_BLOCK = 32  # query tokens per work item
 
 
 def executed_tiles(c: Chunk, *, dense: bool = False) -> int:
-    """64-key tiles the kernel visits per KV head (mirror of its tile schedule)."""
+    """KV tiles the kernel visits per KV head (mirror of its tile schedule)."""
     sb = 0 if dense else SPARSE_BEGIN
     se = 0 if dense else max(0, c.prompt_len - TAIL)
     total = 0

@@ -134,8 +134,8 @@ def test_workspace_sizes(lib):
     for n in (ws(512, 7680, 8192, 8192), dws(512, 7680, 8192)):
         assert n > 0 and n % (8 * PARTIAL_BYTES) == 0
     # a 2048-row chunk already fills the GPU with row blocks: no split ...
-    assert dws(2048, 4096, 6144) == 0
-    # ... unless a row block holds more than 128 tiles (8192 keys), the most one item takes
+    assert dws(2048, 2048, 4096) == 0
+    # ... unless a row block holds more than 128 tiles (4096 keys), the most one item takes
     assert dws(2048, 6272, 8320) > 0
     # invalid attributes -> -1 with a message
     assert ws(0, 0, 0, 0) == -1 and lib.tm_last_error().decode()
