@@ -121,6 +121,8 @@ static_assert(kWaves == 2 * kQuarters && kDmaPerTile == 8,
 // it before a barrier that publishes DMA'd tiles to the other waves -- the
 // barrier alone does not order the DMA's LDS writes.
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// All but the last eight vector-memory operations of this wave have landed.
+__device__ __forceinline__ void wait_dma_but8() { __builtin_amdgcn_s_waitcnt(0x0F78); }
 
 __device__ __forceinline__ int k_slot(int row, int chunk) { return chunk ^ (row & 15); }
 __device__ __forceinline__ int v_slot(int row, int chunk) { return chunk ^ ((row & 3) << 2); }
@@ -241,6 +243,8 @@ triangle_paged_attention_kernel(KernelParams p) {
   __shared__ __attribute__((aligned(1024))) char k_lds1[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) char v_lds0[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) char v_lds1[kSlotBytes];
+  // Q of the workgroup's two heads: [head][row][16-byte slot], K's swizzle.
+  __shared__ __attribute__((aligned(1024))) char q_lds[kHeadsPerGroup * kRowBlock * kRowBytes];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, kept scalar
@@ -308,13 +312,12 @@ triangle_paged_attention_kernel(KernelParams p) {
   // Physical page of every tile of the item (at most kMaxItemTiles = 128):
   // lane i of page_lo / page_hi holds tile i / 64 + i; the loop reads them
   // with v_readlane, so it never waits on a scalar memory load (whose counter
-  // it shares with the LDS reads).  Both these loads and the Q loads below go
-  // through buffer resources whose range ends at the data: an offset past it
-  // reads 0, so no load sits in a divergent branch (the compiler waits for a
-  // load before such a branch joins, which would serialise the round trips).
-  // Order: block table first, then Q, then the tile DMA -- loads complete in
-  // issue order, so the DMA (which needs the page numbers) does not wait for
-  // Q, and Q's latency hides behind the block-table round trip.
+  // it shares with the LDS reads).  The loads go through a buffer resource
+  // whose range ends at the data: an offset past it reads 0, so no load sits
+  // in a divergent branch (the compiler waits for a load before such a branch
+  // joins).  Order: block table, then Q, then the tile DMA -- loads complete
+  // in issue order, so the DMA (which needs the page numbers) does not wait
+  // for Q, and Q's latency hides behind the block-table round trip.
   const int logical_pages = (p.seq_len + kPageSize - 1) / kPageSize;
   const __amdgpu_buffer_rsrc_t bt_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.block_table, (short)0, logical_pages * 4, kBufferFlags);
@@ -325,19 +328,26 @@ triangle_paged_attention_kernel(KernelParams p) {
   };
   const int page_lo = lane_page(lane);
   const int page_hi = lane_page(64 + lane);
-  // ---- Q^T operand: lane (token n, half) holds Q[q][head][16c + 8*half .. +8] ----
-  // The range is the row block's rows: rows past seq_len read 0.
-  bf16x8_t qreg[kHeadDim / 16];
+  // ---- Q: the workgroup's two heads x 32 rows (16 KB), DMA'd once into LDS ----
+  // (each of the four quarter waves of a head needs all of it; loading it per
+  // wave would quadruple the start-up traffic through the CU).  Wave w loads
+  // 1 KB blocks g = 2w, 2w + 1: head g / 8, rows 4 (g % 8) .. + 3; lane i
+  // writes slot i % 16 of row 4 (g % 8) + i / 16, i.e. global chunk
+  // k_slot(row, i % 16).  The range ends at the block's last row: rows past
+  // seq_len read 0.  Issued before the wait on the block table (no dependency).
   {
     const __amdgpu_buffer_rsrc_t q_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.query + (size_t)(tb - p.query_start) * kQueryHeads * kHeadDim), (short)0,
-        (te - tb) * kQueryHeads * kHeadDim * 2, kBufferFlags);
-    const unsigned qoff = (unsigned)(((n * kQueryHeads + head) * kHeadDim + 8 * half) * 2);
+        (void*)(p.query + ((size_t)(tb - p.query_start) * kQueryHeads + kvh * kGroup + kHeadsPerGroup * hp) * kHeadDim),
+        (short)0, (te - tb - 1) * kQueryHeads * kRowBytes + kHeadsPerGroup * kRowBytes, kBufferFlags);
 #pragma unroll
-    for (int c = 0; c < kHeadDim / 16; ++c) {
-      qreg[c] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(q_rsrc, qoff + 32 * c, 0, 0));
+    for (int j = 0; j < 2; ++j) {
+      const int g = 2 * wave + j;
+      const int row = 4 * (g & 7) + (lane >> 4);
+      const unsigned off = (unsigned)(row * kQueryHeads * kRowBytes + (g >> 3) * kRowBytes + 16 * k_slot(row, lane & 15));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rsrc, TM_LDS(q_lds + g * 1024), 16, off, 0, 0, 0);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);  // keep the Q DMA ahead of the K/V DMA (the prologue waits count on it)
 
   auto tile_page = [&](int ti) {
     return __builtin_amdgcn_readlane(ti < 64 ? page_lo : page_hi, ti & 63);
@@ -368,6 +378,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   // Prologue DMA: K and V of iteration 0, K of iteration 1.
   if (dma_t == 0) {
     issue_tile(dma_u, 0, k_lds0 + dma_u * kTileBytes);
+    __builtin_amdgcn_sched_barrier(0);  // K of iteration 1 goes last: the prologue wait leaves it in flight
     issue_tile(kQuarters + dma_u, 0, k_lds1 + dma_u * kTileBytes);
   } else {
     issue_tile(dma_u, 1, v_lds0 + dma_u * kTileBytes);
@@ -423,8 +434,40 @@ triangle_paged_attention_kernel(KernelParams p) {
     }
   };
 
-  wait_dma();
-  __syncthreads();  // prologue DMA of every wave landed
+  // Q and K/V of iteration 0 landed; the K waves' last eight loads (K of
+  // iteration 1, not read before the next barrier) may still be in flight.
+  // Only DMA data is published here, so a bare barrier (no fence: the fence
+  // of __syncthreads would wait for every outstanding load) suffices.
+  if (dma_t == 0) {
+    wait_dma_but8();
+  } else {
+    wait_dma();
+  }
+  __builtin_amdgcn_s_barrier();
+  // Q^T operand: lane (token n, half) holds Q[q][head][16c + 8*half .. +8].
+  // Read in one asm block that waits for its own reads: the compiler cannot
+  // tell q_lds from the K slot the K waves' last DMA still writes, and would
+  // otherwise wait for that DMA here.  The waits above cover the Q DMA (issued
+  // before all K/V DMA).
+  bf16x8_t qreg[kHeadDim / 16];
+  {
+    const unsigned qb = (unsigned)(size_t)TM_LDS(q_lds + hl * kRowBlock * kRowBytes);
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %9\n\t"
+        "ds_read_b128 %2, %10\n\t"
+        "ds_read_b128 %3, %11\n\t"
+        "ds_read_b128 %4, %12\n\t"
+        "ds_read_b128 %5, %13\n\t"
+        "ds_read_b128 %6, %14\n\t"
+        "ds_read_b128 %7, %15\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(qreg[0]), "=&v"(qreg[1]), "=&v"(qreg[2]), "=&v"(qreg[3]), "=&v"(qreg[4]), "=&v"(qreg[5]),
+          "=&v"(qreg[6]), "=&v"(qreg[7])
+        : "v"(qb + k_off[0]), "v"(qb + k_off[1]), "v"(qb + k_off[2]), "v"(qb + k_off[3]), "v"(qb + k_off[4]),
+          "v"(qb + k_off[5]), "v"(qb + k_off[6]), "v"(qb + k_off[7])
+        : "memory");
+  }
   f32x16_t s_a, s_b;
   float m_tile = -INFINITY;  // row max of the tile the next iteration exponentiates (log2 units)
   if (kq < num_tiles) {
