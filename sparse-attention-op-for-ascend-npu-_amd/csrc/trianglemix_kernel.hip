@@ -507,17 +507,23 @@ triangle_paged_attention_kernel(KernelParams p) {
     const float shift = softmax_update(m_tile, m_run, l_run, o_acc);
     // Block 1: the QK^T MFMAs of the next tile (run unconditionally: past the
     // last tile they read a stale slot and the result is unused) interleaved,
-    // in program order, with the exponentials of this tile -- one MFMA, then
-    // two elements' exp / row-sum / bf16 work -- and one prefetch DMA
-    // instruction per step.  K operands are read kReadAhead steps ahead of
+    // in program order, with the exponentials of this tile and one prefetch
+    // DMA instruction per step.  Step k exponentiates element k and, on even
+    // steps, element 8 + k/2 (twelve of the sixteen); block 2 does the last
+    // four before the PV steps that need them, so the VALU work is spread
+    // over both blocks' MFMAs.  K operands are read kReadAhead steps ahead of
     // their MFMA; the last steps also start the V reads of block 2.
     const char* kt = kr + tile_off;
     const char* vt = vr + tile_off;
     bf16x8_t kf[8], va[8];
 #pragma unroll
     for (int k = 0; k < kReadAhead; ++k) kf[k] = k_operand(kt, k_off, k);
-    bf16x8_t pb[2];
+    float px[16];
     float rsum = 0.0f;
+    auto expo = [&](int e) {
+      px[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[e], c2, -shift));
+      rsum += px[e];
+    };
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       dma(pf_rsrc, pf_lds, k);
@@ -527,30 +533,38 @@ triangle_paged_attention_kernel(KernelParams p) {
         va[k + kReadAhead - 8] = v_operand(vt, v_off, k + kReadAhead - 8);
       }
       s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qreg[k], k == 0 ? f32x16_t{} : s_nxt, 0, 0, 0);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int e = 2 * k + t;
-        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[e], c2, -shift));
-        rsum += x;
-        pb[e >> 3][e & 7] = (__bf16)x;
-      }
+      expo(k);
+      if ((k & 1) == 0) expo(8 + (k >> 1));
       __builtin_amdgcn_sched_barrier(0);
     }
-    l_run += rsum;
-    // An empty statement that consumes P here keeps the exponentials in block
-    // 1 (otherwise they sink past the mask branches below, next to their use).
-    asm volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(l_run));
-    // Block 2: the PV MFMAs of this tile interleaved with the row max of the
-    // next one (masked first; its state update opens the next iteration).
+    bf16x8_t pb[2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pb[0][e] = (__bf16)px[e];
+    // An empty statement that consumes these values here keeps the
+    // exponentials in block 1 (otherwise they sink past the mask branches
+    // below, next to their use).
+    asm volatile("" ::"v"(pb[0]), "v"(px[8]), "v"(px[9]), "v"(px[10]), "v"(px[11]), "v"(rsum));
+    // Block 2: the PV MFMAs of this tile interleaved with the last four
+    // exponentials (steps 0-3, before pb[1] is first used at step 4) and the
+    // row max of the next tile (masked first; its state update opens the next
+    // iteration).
     mask_tile(s_nxt, ti + kQuarters);
     float tmax = -INFINITY;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if (k + kReadAhead < 8) va[k + kReadAhead] = v_operand(vt, v_off, k + kReadAhead);
+      if (k < 4) {
+        expo(12 + k);
+        if (k == 3) {
+#pragma unroll
+          for (int e = 8; e < 16; ++e) pb[1][e - 8] = (__bf16)px[e];
+        }
+      }
       o_acc[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[k], pb[k >> 2], o_acc[k & 3], 0, 0, 0);
       tmax = fmaxf(tmax, fmaxf(s_nxt[2 * k], s_nxt[2 * k + 1]));
       __builtin_amdgcn_sched_barrier(0);
     }
+    l_run += rsum;
     m_tile = fmaxf(tmax, other_half(tmax)) * c2;
   };
   for (int it = 0; it < num_iters; it += 2) {
