@@ -116,8 +116,12 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   if (!std::isfinite(scale) || scale <= 0.0f) {
     return fail(TM_ERR_INVALID_ARGUMENT, "invalid query_start/seq_len/prompt_len/scale attributes");
   }
-  if (num_pages <= 0 || num_pages > (int64_t(1) << 31) - 1) {
+  if (num_pages <= 0) {
     return fail(TM_ERR_INVALID_ARGUMENT, "key_cache must be [pages, 128, 8, 128] with pages > 0");
+  }
+  if (num_pages > tmx::kMaxPages) {
+    return fail(TM_ERR_UNSUPPORTED, "key_cache has %lld pages; the limit is %lld", (long long)num_pages,
+                (long long)tmx::kMaxPages);
   }
   const int64_t required_pages = (seq_len + tmx::kPageSize - 1) / tmx::kPageSize;
   if (block_table_cols < required_pages) {

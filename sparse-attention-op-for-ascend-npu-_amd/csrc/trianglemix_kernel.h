@@ -33,6 +33,10 @@ constexpr int64_t kPartialBytes = kPartialFloats * 4;
 // Largest number of tiles one work item may hold: the kernel keeps the item's
 // page numbers in two 64-lane registers.  Longer rows are split.
 constexpr int kMaxItemTiles = 128;
+// Most cache pages a launch accepts: the kernel addresses a key row of one KV
+// head by a 32-bit row index (page * 128 + slot) * 8 + head.  2^22 pages of
+// 256 KB per K or V cache are more than one GPU's memory.
+constexpr int64_t kMaxPages = int64_t(1) << 22;
 
 // Largest seq_len / prompt_len the 32-bit position arithmetic accepts.
 constexpr int64_t kMaxPositions = (int64_t(1) << 30);

@@ -309,25 +309,30 @@ triangle_paged_attention_kernel(KernelParams p) {
     const int slot = dma_t == 0 ? k_slot(row, lane & 15) : v_slot(row, lane & 15);
     dma_voff[j] = (unsigned)(row * kKvHeads * kRowBytes + 16 * slot);
   }
-  // Physical page of every tile of the item (at most kMaxItemTiles = 128):
-  // lane i of page_lo / page_hi holds tile i / 64 + i; the loop reads them
-  // with v_readlane, so it never waits on a scalar memory load (whose counter
-  // it shares with the LDS reads).  The loads go through a buffer resource
-  // whose range ends at the data: an offset past it reads 0, so no load sits
-  // in a divergent branch (the compiler waits for a load before such a branch
-  // joins).  Order: block table, then Q, then the tile DMA -- loads complete
-  // in issue order, so the DMA (which needs the page numbers) does not wait
-  // for Q, and Q's latency hides behind the block-table round trip.
+  // DMA source of every tile of the item (at most kMaxItemTiles = 128): lane
+  // i of row_lo holds tile i, lane i of row_hi tile 64 + i.  The value is the
+  // cache row index of the tile's first key row of this KV head (its byte
+  // offset / 256, below 2^32 as the host caps the cache at kMaxPages pages);
+  // bytes_lo / bytes_hi hold the tile's valid byte count (rows cut at seq_len,
+  // 0 past the item's end).  The loop reads them with v_readlane -- it never
+  // waits on a scalar memory load (whose counter it shares with the LDS reads)
+  // and builds a buffer resource in a few scalar instructions.  The
+  // block-table loads go through a buffer resource whose range ends at the
+  // data: an offset past it reads 0, so no load sits in a divergent branch
+  // (the compiler waits for a load before such a branch joins).  Order: block
+  // table, then Q, then the tile DMA -- loads complete in issue order, so the
+  // DMA (which needs the page numbers) does not wait for Q, and Q's latency
+  // hides behind the block-table round trip.
   const int logical_pages = (p.seq_len + kPageSize - 1) / kPageSize;
   const __amdgpu_buffer_rsrc_t bt_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.block_table, (short)0, logical_pages * 4, kBufferFlags);
+  auto lane_k0 = [&](int ti) { return ti < num_tiles ? runs.tile(t_lo + ti) * kKvTile : 0; };
   auto lane_page = [&](int ti) {
-    const unsigned off = ti < num_tiles ? (unsigned)(runs.tile(t_lo + ti) * kKvTile / kPageSize) * 4u : kOutOfRange;
-    const int phys = __builtin_amdgcn_raw_buffer_load_b32(bt_rsrc, off, 0, 0);
-    return min(max(phys, 0), p.num_pages - 1);
+    const unsigned off = ti < num_tiles ? (unsigned)(lane_k0(ti) / kPageSize) * 4u : kOutOfRange;
+    return __builtin_amdgcn_raw_buffer_load_b32(bt_rsrc, off, 0, 0);
   };
-  const int page_lo = lane_page(lane);
-  const int page_hi = lane_page(64 + lane);
+  const int phys_lo = lane_page(lane);
+  const int phys_hi = lane_page(64 + lane);
   // ---- Q: the workgroup's two heads x 32 rows (16 KB), DMA'd once into LDS ----
   // (each of the four quarter waves of a head needs all of it; loading it per
   // wave would quadruple the start-up traffic through the CU).  Wave w loads
@@ -349,21 +354,26 @@ triangle_paged_attention_kernel(KernelParams p) {
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the Q DMA ahead of the K/V DMA (the prologue waits count on it)
 
-  auto tile_page = [&](int ti) {
-    return __builtin_amdgcn_readlane(ti < 64 ? page_lo : page_hi, ti & 63);
+  auto lane_row = [&](int ti, int phys) {
+    phys = min(max(phys, 0), p.num_pages - 1);
+    return ((unsigned)phys * kPageSize + (unsigned)(lane_k0(ti) % kPageSize)) * kKvHeads + kvh;
   };
+  auto lane_bytes = [&](int ti) {
+    const int valid_rows = ti < num_tiles ? min(kKvTile, p.seq_len - lane_k0(ti)) : 0;
+    return valid_rows > 0 ? (valid_rows - 1) * kKvHeads * kRowBytes + kRowBytes : 0;
+  };
+  const unsigned row_lo = lane_row(lane, phys_lo);
+  const unsigned row_hi = lane_row(64 + lane, phys_hi);
+  const int bytes_lo = lane_bytes(lane);
+  const int bytes_hi = lane_bytes(64 + lane);
   // Buffer resource of tensor t (0 = K, 1 = V) of tile ti: the tile's key rows
   // of this KV head, range cut at seq_len; a tile past the item's end gets an
   // empty range (its loads return zeros).
   auto tile_rsrc = [&](int ti, int t) {
-    const bool live = ti < num_tiles;
-    const int phys = tile_page(ti);
-    const int k0 = live ? runs.tile(t_lo + ti) * kKvTile : 0;
-    const size_t first_row = (((size_t)phys * kPageSize + (k0 % kPageSize)) * kKvHeads + kvh) * kHeadDim;
-    const int valid_rows = live ? min(kKvTile, p.seq_len - k0) : 0;
-    const int bytes = valid_rows > 0 ? (valid_rows - 1) * kKvHeads * kRowBytes + kRowBytes : 0;
-    const __bf16* cache = t == 0 ? p.key_cache : p.value_cache;
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(cache + first_row), (short)0, bytes, kBufferFlags);
+    const unsigned row = __builtin_amdgcn_readlane(ti < 64 ? row_lo : row_hi, ti & 63);
+    const int bytes = ti < num_tiles ? __builtin_amdgcn_readlane(ti < 64 ? bytes_lo : bytes_hi, ti & 63) : 0;
+    const char* cache = reinterpret_cast<const char*>(t == 0 ? p.key_cache : p.value_cache);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(cache + (size_t)row * kRowBytes), (short)0, bytes, kBufferFlags);
   };
   // DMA instruction j of this wave's tile of one iteration.
   auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, char* lds_tile, int j) {
@@ -482,6 +492,9 @@ triangle_paged_attention_kernel(KernelParams p) {
     for (int v = 0; v < 16; ++v) tmax = fmaxf(tmax, s_a[v]);
     m_tile = fmaxf(tmax, other_half(tmax)) * c2;
   }
+  // O and the row sum are still zero: the first tile's max becomes the state
+  // directly (the first update then rescales nothing).
+  m_run = m_tile;
 
   // Iteration it (this wave's tile ti = 4*it + kq): state update with tile
   // ti's row max, then [QK^T of tile ti+4 (K slot kr) || exponentials of tile

@@ -95,6 +95,7 @@ def _sparse(lib, **over):
     (dict(scale=float("nan")), 1, "scale"),
     (dict(scale=float("inf")), 1, "scale"),
     (dict(pages=0), 1, "pages > 0"),
+    (dict(pages=(1 << 22) + 1), 2, "limit is 4194304"),
     (dict(cols=35), 1, "block_table lacks"),
     (dict(out=Q + 1024), 1, "must not overlap"),
     (dict(out=K + 4096), 1, "must not overlap"),
