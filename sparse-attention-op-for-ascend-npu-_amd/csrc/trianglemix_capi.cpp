@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <vector>
 #include <cstring>
 
 #include "../../include/trianglemix.h"
@@ -55,15 +56,93 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
   return TM_OK;
 }
 
-// Split-KV sizing: cut long row blocks so that the chunk's tiles spread
-// evenly over kTargetItemsPerHead items per KV head -- each item runs as two
-// workgroups of one CU each, so 16 items per head give every one of the 256
-// CUs about the same number of tiles in one round -- and never cut a row block
-// into pieces of fewer than kMinSplitTiles tiles (1024 keys): a split's fp32
-// partial (66 KB) must stay small next to the K/V it reads (16 KB per 32-key
-// tile).  The heaviest items are issued first.
-constexpr int kTargetItemsPerHead = 16;
+// Split-KV sizing.  A chunk runs as 16 workgroups (8 KV heads x 2 head
+// pairs) per work item, one workgroup per CU, so each (KV head, head pair)
+// has kSlots of the 256 CUs.  A row block of n tiles is cut into
+// ceil(n / T) near-equal items of at most T tiles; T is chosen by simulating
+// the greedy dispatch of the items (issued heaviest row block first) onto
+// kSlots slots, an item costing kItemFixedTiles + its tiles, and taking the T
+// with the shortest makespan (ties: larger T, fewer partials).  T is at least
+// kMinSplitTiles (1024 keys: a split's fp32 partial of 66 KB stays small next
+// to the K/V it reads, 16 KB per 32-key tile) and at most kMaxItemTiles.
+constexpr int kSlots = 16;
+constexpr int kItemFixedTiles = 15;  // start-up, merge and store of an item, in tile times (measured)
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
+// Beyond this many items per candidate the simulation is skipped (its host
+// cost would show): T then spreads the chunk's tiles over kSlots items.
+constexpr int64_t kMaxSimulatedItems = 4096;
+constexpr int kSplitStep = 4;  // candidate T: kMaxItemTiles, kMaxItemTiles - 4, ..., >= kMinSplitTiles
+
+int64_t simulated_makespan(const std::vector<int>& row_tiles, int T) {
+  int64_t slot[kSlots] = {};
+  for (const int n : row_tiles) {
+    const int pieces = (n + T - 1) / T;
+    for (int i = 0; i < pieces; ++i) {
+      const int size = (int)((int64_t)(i + 1) * n / pieces - (int64_t)i * n / pieces);
+      int best = 0;
+      for (int k = 1; k < kSlots; ++k) best = slot[k] < slot[best] ? k : best;
+      slot[best] += kItemFixedTiles + size;
+    }
+  }
+  int64_t makespan = 0;
+  for (const int64_t f : slot) makespan = f > makespan ? f : makespan;
+  return makespan;
+}
+
+int choose_tiles_per_split(const std::vector<int>& row_tiles) {
+  int64_t total = 0;
+  int longest = 0;
+  for (const int n : row_tiles) {
+    total += n;
+    longest = n > longest ? n : longest;
+  }
+  if (longest <= kMinSplitTiles) return kMinSplitTiles;  // nothing to split
+  if (total / kMinSplitTiles > kMaxSimulatedItems) {
+    const int64_t per_item = (total + kSlots - 1) / kSlots;
+    return (int)(per_item < kMinSplitTiles ? kMinSplitTiles : (per_item > tmx::kMaxItemTiles ? tmx::kMaxItemTiles : per_item));
+  }
+  int best_t = tmx::kMaxItemTiles;
+  int64_t best = simulated_makespan(row_tiles, best_t);
+  for (int t = tmx::kMaxItemTiles - kSplitStep; t >= kMinSplitTiles; t -= kSplitStep) {
+    const int64_t ms = simulated_makespan(row_tiles, t);
+    if (ms < best) {
+      best = ms;
+      best_t = t;
+    }
+  }
+  return best_t;
+}
+
+// The choice depends only on the chunk geometry, which repeats for every layer
+// of a step: a small per-thread cache keeps the simulation off the launch path.
+struct PlanKey {
+  int64_t num_row_blocks, query_start, seq_len, sparse_begin, sparse_end;
+  bool operator==(const PlanKey& o) const {
+    return num_row_blocks == o.num_row_blocks && query_start == o.query_start && seq_len == o.seq_len &&
+           sparse_begin == o.sparse_begin && sparse_end == o.sparse_end;
+  }
+};
+
+int cached_tiles_per_split(const PlanKey& key) {
+  constexpr int kEntries = 8;
+  thread_local PlanKey keys[kEntries];
+  thread_local int values[kEntries];
+  thread_local int used = 0, next = 0;
+  for (int i = 0; i < used; ++i) {
+    if (keys[i] == key) return values[i];
+  }
+  std::vector<int> row_tiles((size_t)key.num_row_blocks);
+  for (int64_t o = 0; o < key.num_row_blocks; ++o) {
+    row_tiles[(size_t)o] = tmx::row_block_splits((int)o, (int)key.num_row_blocks, (int)key.query_start,
+                                                 (int)key.seq_len, (int)key.sparse_begin, (int)key.sparse_end, 1);
+  }
+  const int t = choose_tiles_per_split(row_tiles);
+  keys[next] = key;
+  values[next] = t;
+  next = (next + 1) % kEntries;
+  used = used < kEntries ? used + 1 : used;
+  return t;
+}
 
 // Work items per KV head beyond which a launch is refused (its grid would
 // exceed 2^30 workgroups).
@@ -81,14 +160,8 @@ Geometry make_geometry(bool sparse, int64_t query_tokens, int64_t query_start, i
   g.sparse_begin = sparse ? tmx::kSparseBegin : 0;
   g.sparse_end = sparse ? (int)(prompt_len > tmx::kDenseTail ? prompt_len - tmx::kDenseTail : 0) : 0;
   g.num_row_blocks = (int)((query_tokens + tmx::kRowBlock - 1) / tmx::kRowBlock);
-  int64_t total_tiles = 0;
-  for (int o = 0; o < g.num_row_blocks; ++o) {
-    total_tiles += tmx::row_block_splits(o, g.num_row_blocks, (int)query_start, (int)seq_len, g.sparse_begin,
-                                         g.sparse_end, 1);
-  }
-  const int64_t per_item = (total_tiles + kTargetItemsPerHead - 1) / kTargetItemsPerHead;
-  g.tiles_per_split = (int)(per_item > kMinSplitTiles ? per_item : kMinSplitTiles);
-  if (g.tiles_per_split > tmx::kMaxItemTiles) g.tiles_per_split = tmx::kMaxItemTiles;
+  g.tiles_per_split = cached_tiles_per_split(
+      PlanKey{g.num_row_blocks, query_start, seq_len, g.sparse_begin, g.sparse_end});
   bool any_split = false;
   int64_t items = 0;
   for (int o = 0; o < g.num_row_blocks; ++o) {

@@ -481,11 +481,14 @@ triangle_paged_attention_kernel(KernelParams p) {
   f32x16_t s_a, s_b;
   float m_tile = -INFINITY;  // row max of the tile the next iteration exponentiates (log2 units)
   if (kq < num_tiles) {
+    // All eight K operands are read before the MFMA chain starts.
+    bf16x8_t k0f[kHeadDim / 16];
+#pragma unroll
+    for (int c = 0; c < kHeadDim / 16; ++c) k0f[c] = k_operand(k_lds0 + tile_off, k_off, c);
+    __builtin_amdgcn_sched_barrier(0);
     s_a = f32x16_t{};
 #pragma unroll
-    for (int c = 0; c < kHeadDim / 16; ++c) {
-      s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_operand(k_lds0 + tile_off, k_off, c), qreg[c], s_a, 0, 0, 0);
-    }
+    for (int c = 0; c < kHeadDim / 16; ++c) s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k0f[c], qreg[c], s_a, 0, 0, 0);
     mask_tile(s_a, kq);
     float tmax = -INFINITY;
 #pragma unroll
@@ -674,24 +677,25 @@ triangle_paged_attention_kernel(KernelParams p) {
 
 // Merge the split-KV partials of every split row block with the online-
 // softmax rescale rule, then normalise and write bf16.  One workgroup per
-// (row block, KV head) with one wave per query head of the group; unsplit
-// row blocks exit.  The partials' row maxima are read first, so the O loads
-// of all splits are independent of each other and stay in flight together;
-// the weighted sums run in split order (deterministic).
-constexpr int kCombineThreads = kGroup * 64;
+// (row block, KV head, query head of the group) with one wave per 32-wide
+// d-block; unsplit row blocks exit.  Each wave reads the row maxima and row
+// sums of all splits first, then the O partials eight splits at a time, so
+// the loads of a batch are independent of each other and stay in flight
+// together; the weighted sums run in split order (deterministic).
+constexpr int kCombineThreads = (kHeadDim / 32) * 64;
+constexpr int kCombineBatch = 8;
 
-// Occupancy is not the limit here (one small workgroup per split row block):
-// let the compiler keep every load of a split in flight.
 template <bool kSparse>
-__global__ void __launch_bounds__(kCombineThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+__global__ void __launch_bounds__(kCombineThreads)
 triangle_paged_attention_combine_kernel(KernelParams p) {
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int m = tid >> 6;  // d-block
   const int lane = tid & 63;
   const int n = lane & 31;
   const int half = lane >> 5;
   const int kvh = blockIdx.x % kKvHeads;
-  const int order = blockIdx.x / kKvHeads;
+  const int hq = (blockIdx.x / kKvHeads) % kGroup;
+  const int order = blockIdx.x / (kKvHeads * kGroup);
   const int sparse_begin = kSparse ? p.sparse_begin : 0;
   const int sparse_end = kSparse ? p.sparse_end : 0;
 
@@ -717,49 +721,57 @@ triangle_paged_attention_combine_kernel(KernelParams p) {
       first_item += __shfl(incl, 63);
     }
   }
+  first_item = __builtin_amdgcn_readfirstlane(first_item);
+  nsplit = __builtin_amdgcn_readfirstlane(nsplit);
   if (nsplit == 1) return;
 
   const int rb = p.num_row_blocks - 1 - order;
   const int q = p.query_start + rb * kRowBlock + n;
   const bool row_active = q < p.seq_len;
-  const int head = kvh * kGroup + wave;
+  const int head = kvh * kGroup + hq;
   const float* base = p.partials + ((size_t)kvh * p.items_per_head + first_item) * kPartialFloats;
+  const int m_off = kGroup * 64 * 64 + hq * 64 + lane;  // row max of this lane's row
+  const int l_off = kGroup * 64 * 65 + hq * 64 + lane;  // this lane's partial row sum
 
   float mt = -INFINITY;
 #pragma unroll 8
-  for (int s = 0; s < nsplit; ++s) mt = fmaxf(mt, base[s * kPartialFloats + kGroup * 64 * 64 + wave * 64 + lane]);
+  for (int s = 0; s < nsplit; ++s) mt = fmaxf(mt, base[(size_t)s * kPartialFloats + m_off]);
   const float mu = mt == -INFINITY ? 0.0f : mt;
 
   float lt = 0.0f;
-  f32x4_t ot[kHeadDim / 8];  // [m][v/4], 4 consecutive v each
+  f32x4_t ot[4] = {};  // [v/4] of d-block m, 4 consecutive v each
+  for (int s0 = 0; s0 < nsplit; s0 += kCombineBatch) {
+    f32x4_t os[kCombineBatch][4];
+    float w[kCombineBatch], ls[kCombineBatch];
 #pragma unroll
-  for (int i = 0; i < kHeadDim / 8; ++i) ot[i] = f32x4_t{};
-  for (int s = 0; s < nsplit; ++s) {
-    const float* part = base + s * kPartialFloats;
-    // All 16 vector loads of the split first, then the arithmetic.
-    f32x4_t os[kHeadDim / 8];
+    for (int b = 0; b < kCombineBatch; ++b) {
+      const int s = min(s0 + b, nsplit - 1);  // past the last split: a repeated load, weighted 0 below
+      const float* part = base + (size_t)s * kPartialFloats;
 #pragma unroll
-    for (int i = 0; i < kHeadDim / 8; ++i) {
-      os[i] = *reinterpret_cast<const f32x4_t*>(part + ((wave * 16 + i) * 64 + lane) * 4);
+      for (int g = 0; g < 4; ++g) {
+        os[b][g] = *reinterpret_cast<const f32x4_t*>(part + (((hq * 4 + m) * 4 + g) * 64 + lane) * 4);
+      }
+      w[b] = part[m_off];
+      ls[b] = part[l_off];
     }
-    const float w = __builtin_amdgcn_exp2f(part[kGroup * 64 * 64 + wave * 64 + lane] - mu);
-    lt += part[kGroup * 64 * 65 + wave * 64 + lane] * w;
 #pragma unroll
-    for (int i = 0; i < kHeadDim / 8; ++i) ot[i] += os[i] * w;
+    for (int b = 0; b < kCombineBatch; ++b) {
+      const float wb = s0 + b < nsplit ? __builtin_amdgcn_exp2f(w[b] - mu) : 0.0f;
+      lt += ls[b] * wb;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) ot[g] += os[b][g] * wb;
+    }
   }
   const float l_tot = lt + other_half(lt);  // the two 32-lane halves hold one row
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (!row_active) return;
   __bf16* orow = p.out + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim;
 #pragma unroll
-  for (int m = 0; m < kHeadDim / 32; ++m) {
+  for (int g = 0; g < 4; ++g) {
+    bf16x4_t o4;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      bf16x4_t o4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(ot[4 * m + g][e] * inv);
-      *reinterpret_cast<bf16x4_t*>(orow + 32 * m + 8 * g + 4 * half) = o4;
-    }
+    for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(ot[g][e] * inv);
+    *reinterpret_cast<bf16x4_t*>(orow + 32 * m + 8 * g + 4 * half) = o4;
   }
 }
 
@@ -770,8 +782,8 @@ hipError_t launch(const KernelParams& p, bool any_split, hipStream_t stream) {
                      p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !any_split) return err;
-  hipLaunchKernelGGL(triangle_paged_attention_combine_kernel<kSparse>, dim3((unsigned)(p.num_row_blocks * kKvHeads)),
-                     dim3(kCombineThreads), 0, stream, p);
+  hipLaunchKernelGGL(triangle_paged_attention_combine_kernel<kSparse>,
+                     dim3((unsigned)(p.num_row_blocks * kKvHeads * kGroup)), dim3(kCombineThreads), 0, stream, p);
   return hipGetLastError();
 }
 
