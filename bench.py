@@ -16,6 +16,10 @@ Reported JSON line (rank 0 only):
   for this workload exists under profiles/, else null;
 * ``dense`` -- the same 16 chunks through the dense paged causal companion
   kernel, and the attention-time cut of sparse vs dense (ABBA order);
+* ``kv_write`` -- the paged KV write upstream of the attention
+  (``trianglemix::reshape_and_cache``): one chunk's fresh K/V into its pages,
+  and the whole prompt in one call, with HBM GB/s against 8 TB/s (it moves
+  each token's 2 KB K row and 2 KB V row in and out);
 * ``cpu_baseline`` -- the fp32 PyTorch CPU masked-attention restatement of the
   reference's oracle (``oracle.attention.attention_torch``) over all 16
   chunks, median of 2 passes after a warm-up, on this host's cores.
@@ -191,6 +195,8 @@ def main() -> int:
 
     traffic = read_traffic_summary()
 
+    kv_write = kv_write_bench(args, chunks, k, v, bt, dev) if args.only is None else None
+
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
         cpu = cpu_baseline(chunks, qfull, k, v, bt, SCALE)
@@ -232,10 +238,63 @@ def main() -> int:
             "alg_tflops": round(dense_flops / (ms_dense * 1e-3) / 1e12, 2) if ms_dense == ms_dense else None,
             "attention_time_cut": round(1.0 - ms_sparse / ms_dense, 4) if ms_dense == ms_dense else None,
         },
+        "kv_write": kv_write,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def kv_write_bench(args, chunks, k, v, bt, dev):
+    """Paged KV write: µs and HBM GB/s for one chunk and for the whole prompt (checked against the cache)."""
+    import torch
+
+    from trianglemix.cache import chunk_slot_mapping
+
+    table = bt[0].tolist()
+    logical = torch.tensor([table[t // 128] * 128 + t % 128 for t in range(args.prompt)], dtype=torch.int64)
+    k_tok = k.view(-1, 8, 128)[logical].to(dev)  # each token's fresh K / V, in logical order
+    v_tok = v.view(-1, 8, 128)[logical].to(dev)
+    btd = bt.to(dev)
+    kc = torch.zeros(k.shape, dtype=k.dtype, device=dev)
+    vc = torch.zeros_like(kc)
+    op = torch.ops.trianglemix.reshape_and_cache
+    slots = [chunk_slot_mapping(btd, c.query_start, c.query_tokens) for c in chunks]
+    for c, sl in zip(chunks, slots):  # fill chunk by chunk, as the prefill does
+        op(k_tok[c.query_start:c.seq_len], v_tok[c.query_start:c.seq_len], kc, vc, sl)
+    torch.cuda.synchronize()
+    if not (torch.equal(kc.view(-1, 8, 128)[logical.to(dev)], k_tok) and
+            torch.equal(vc.view(-1, 8, 128)[logical.to(dev)], v_tok)):
+        raise RuntimeError("paged KV write does not reproduce the cache")
+
+    def per_call_us(fn, reps=50):
+        fn()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1000.0 / reps
+
+    c0, s0 = chunks[len(chunks) // 2], slots[len(chunks) // 2]
+    us_chunk = per_call_us(lambda: op(k_tok[c0.query_start:c0.seq_len], v_tok[c0.query_start:c0.seq_len], kc, vc, s0))
+    all_slots = chunk_slot_mapping(btd, 0, args.prompt)
+    us_prompt = per_call_us(lambda: op(k_tok, v_tok, kc, vc, all_slots))
+    moved = lambda tokens: tokens * 8 * 128 * 2 * 2 * 2  # K and V rows, read and written
+    gbs_chunk = moved(c0.query_tokens) / (us_chunk * 1e-6) / 1e9
+    gbs_prompt = moved(args.prompt) / (us_prompt * 1e-6) / 1e9
+    return {
+        "chunk_tokens": c0.query_tokens,
+        "us_per_chunk": round(us_chunk, 2),
+        "gbs_chunk": round(gbs_chunk, 1),
+        "prompt_tokens": args.prompt,
+        "us_prompt": round(us_prompt, 2),
+        "gbs_prompt": round(gbs_prompt, 1),
+        "peak_gbs": PEAK_HBM_GBS,
+        "frac_hbm_prompt": round(gbs_prompt / PEAK_HBM_GBS, 4),
+    }
 
 
 def read_traffic_summary():

@@ -108,6 +108,27 @@ int tm_dense_paged_causal_attention(
 int64_t tm_dense_paged_causal_attention_workspace_size(
     int64_t query_tokens, int64_t query_start, int64_t seq_len);
 
+/*
+ * Paged KV write, upstream of the attention: scatters one chunk's fresh K and
+ * V rows into their cache slots.  key / value: [num_tokens, 8, 128] bf16 with
+ * the [8, 128] part contiguous and a row stride of key_stride / value_stride
+ * elements (>= 1024, multiples of 8; a slice of a fused QKV buffer works).
+ * slot_mapping: int64 [num_tokens]; token i goes to page slot_mapping[i] / 128,
+ * offset slot_mapping[i] % 128 of both caches.  A negative slot is padding and
+ * is skipped, as is a slot >= num_pages * 128.  Pointers 16-byte aligned; the
+ * caches must not overlap each other or the sources.  num_tokens == 0 enqueues
+ * nothing.
+ *
+ * Replaces vLLM's reshape_and_cache on this page layout (the step that fills
+ * a chunk's pages before they are attended; the reference leaves it to the
+ * engine, planning.py:79-83, and fills pages in its harness by the same page
+ * / offset rule, operator/tests/npu_v2_correctness.py:385-398).
+ */
+int tm_reshape_and_cache(
+    const void* key, const void* value, void* key_cache, void* value_cache,
+    const int64_t* slot_mapping, int64_t num_tokens, int64_t key_stride,
+    int64_t value_stride, int64_t num_pages, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

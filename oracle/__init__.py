@@ -11,6 +11,8 @@ Modules:
 
 * ``geometry``  -- integer restatement of the reference's mask, span, interval,
   page-address and work-accounting rules (pure Python).
+* ``cache``     -- the paged KV write upstream of the attention (slot of a
+  logical token, scatter of a chunk's K/V rows into their pages).
 * ``attention`` -- floating-point restatement of the reference's masked paged
   GQA attention: a float64 numpy version for small cases and a float32
   PyTorch CPU version (the reference's own oracle method) for larger ones.

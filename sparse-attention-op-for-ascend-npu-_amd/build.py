@@ -69,7 +69,7 @@ def build_hip_library() -> Path:
     hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
     tmp = HIP_LIB.with_suffix(".so.tmp")
     _run([hipcc, *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
-          str(CSRC / "trianglemix_kernel.hip"), str(CSRC / "trianglemix_capi.cpp"),
+          str(CSRC / "trianglemix_kernel.hip"), str(CSRC / "trianglemix_cache.hip"), str(CSRC / "trianglemix_capi.cpp"),
           "-o", str(tmp)])
     _atomic_replace(tmp, HIP_LIB)
     return HIP_LIB

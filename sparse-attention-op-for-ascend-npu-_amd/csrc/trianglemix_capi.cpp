@@ -306,4 +306,53 @@ int64_t tm_dense_paged_causal_attention_workspace_size(int64_t query_tokens, int
   return make_geometry(false, query_tokens, query_start, seq_len, seq_len).workspace_bytes;
 }
 
+int tm_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
+                         const int64_t* slot_mapping, int64_t num_tokens, int64_t key_stride, int64_t value_stride,
+                         int64_t num_pages, void* stream) {
+  g_last_error[0] = '\0';
+  if (num_tokens < 0 || num_tokens > tmx::kMaxPositions) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "key and value must be [num_tokens, 8, 128] with 0 <= num_tokens <= %lld",
+                (long long)tmx::kMaxPositions);
+  }
+  if (num_pages <= 0) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "key_cache must be [pages, 128, 8, 128] with pages > 0");
+  }
+  if (num_pages > tmx::kMaxPages) {
+    return fail(TM_ERR_UNSUPPORTED, "key_cache has %lld pages; the limit is %lld", (long long)num_pages,
+                (long long)tmx::kMaxPages);
+  }
+  if (num_tokens == 0) return TM_OK;  // nothing to write, nothing enqueued
+  if (!key || !value || !key_cache || !value_cache || !slot_mapping) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "key, value, key_cache, value_cache and slot_mapping must be non-null");
+  }
+  constexpr int64_t kRowElems = int64_t(tmx::kKvHeads) * tmx::kHeadDim;
+  if (key_stride < kRowElems || value_stride < kRowElems || key_stride % 8 != 0 || value_stride % 8 != 0) {
+    return fail(TM_ERR_INVALID_ARGUMENT,
+                "key and value rows must hold [8, 128] contiguous elements with a row stride >= 1024 that is a "
+                "multiple of 8");
+  }
+  const uintptr_t misaligned = ((uintptr_t)key | (uintptr_t)value | (uintptr_t)key_cache | (uintptr_t)value_cache) & 15;
+  if (misaligned) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "key, value and the caches must be 16-byte aligned");
+  }
+  // The caches are written: they must not overlap each other, the sources or the slot mapping.
+  const Range r_k{(uintptr_t)key, (uintptr_t)key + uintptr_t(((num_tokens - 1) * key_stride + kRowElems) * 2)};
+  const Range r_v{(uintptr_t)value, (uintptr_t)value + uintptr_t(((num_tokens - 1) * value_stride + kRowElems) * 2)};
+  const Range r_kc{(uintptr_t)key_cache, (uintptr_t)key_cache + uintptr_t(num_pages * kPageBytes)};
+  const Range r_vc{(uintptr_t)value_cache, (uintptr_t)value_cache + uintptr_t(num_pages * kPageBytes)};
+  const Range r_s{(uintptr_t)slot_mapping, (uintptr_t)slot_mapping + uintptr_t(num_tokens * 8)};
+  if (overlaps(r_kc, r_vc) || overlaps(r_kc, r_k) || overlaps(r_kc, r_v) || overlaps(r_kc, r_s) ||
+      overlaps(r_vc, r_k) || overlaps(r_vc, r_v) || overlaps(r_vc, r_s)) {
+    return fail(TM_ERR_INVALID_ARGUMENT,
+                "key_cache and value_cache must not overlap each other, key, value or slot_mapping");
+  }
+  const hipError_t err = tmx::launch_paged_kv_write(key, value, key_cache, value_cache, slot_mapping, num_tokens,
+                                                    key_stride, value_stride, num_pages,
+                                                    static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) {
+    return fail(TM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  }
+  return TM_OK;
+}
+
 }  // extern "C"

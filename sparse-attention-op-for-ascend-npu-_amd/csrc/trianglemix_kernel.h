@@ -100,6 +100,14 @@ struct KernelParams {
 // merges its partials (same stream, in order).
 hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, bool any_split, hipStream_t stream);
 
+// Enqueues the paged KV write: token i's K and V rows ([8, 128] bf16, row
+// strides key_stride / value_stride in elements, multiples of 8) go to cache
+// slot slot_mapping[i] (page slot / 128, offset slot % 128); negative slots
+// and slots past num_pages * 128 are skipped.
+hipError_t launch_paged_kv_write(const void* key, const void* value, void* key_cache, void* value_cache,
+                                 const int64_t* slot_mapping, int64_t num_tokens, int64_t key_stride,
+                                 int64_t value_stride, int64_t num_pages, hipStream_t stream);
+
 }  // namespace tmx
 
 #endif  // TRIANGLEMIX_KERNEL_H

@@ -17,6 +17,11 @@
 //   trianglemix::dense_paged_causal_attention.out(q, k, v, bt, query_start, seq_len, scale, *, out)
 //   trianglemix_reference::dense_paged_causal_attention(q, k, v, bt, query_start, seq_len, scale)
 //
+// and the paged KV write upstream of them (vLLM's reshape_and_cache on this
+// page layout, bf16 only):
+//
+//   trianglemix::reshape_and_cache(key, value, key_cache!, value_cache!, slot_mapping) -> ()
+//
 // Input and output checks restate check_inputs / check_output (:29-97) with
 // the same predicates and messages ("GPU" for "NPU").  Launches go on the
 // current HIP stream of the query's device under a device guard, with no
@@ -161,6 +166,52 @@ at::Tensor& dense_paged_causal_attention_out(const at::Tensor& query, const at::
   return output;
 }
 
+// Paged KV write: token i's K / V rows go to cache slot slot_mapping[i]
+// (negative = padding, skipped).  key / value may be row-strided views (a
+// slice of a fused QKV buffer); their [8, 128] part must be contiguous.
+void reshape_and_cache(const at::Tensor& key, const at::Tensor& value, at::Tensor& key_cache, at::Tensor& value_cache,
+                       const at::Tensor& slot_mapping) {
+  TORCH_CHECK(key.is_cuda() && value.is_cuda() && key_cache.is_cuda() && value_cache.is_cuda() &&
+                  slot_mapping.is_cuda(),
+              "key, value, key_cache, value_cache and slot_mapping must be GPU tensors");
+  TORCH_CHECK(key.device() == value.device() && key.device() == key_cache.device() &&
+                  key.device() == value_cache.device() && key.device() == slot_mapping.device(),
+              "all inputs must be on the same GPU device");
+  TORCH_CHECK(key.scalar_type() == at::ScalarType::BFloat16 && value.scalar_type() == at::ScalarType::BFloat16 &&
+                  key_cache.scalar_type() == at::ScalarType::BFloat16 &&
+                  value_cache.scalar_type() == at::ScalarType::BFloat16,
+              "key, value, key_cache and value_cache must be BF16");
+  TORCH_CHECK(slot_mapping.scalar_type() == at::ScalarType::Long && slot_mapping.dim() == 1 &&
+                  slot_mapping.is_contiguous(),
+              "slot_mapping must be a contiguous INT64 [num_tokens] tensor");
+  TORCH_CHECK(key.dim() == 3 && key.size(1) == 8 && key.size(2) == 128 && value.sizes() == key.sizes(),
+              "key and value must be [num_tokens, 8, 128]");
+  TORCH_CHECK(key.size(0) == slot_mapping.size(0), "slot_mapping must hold one slot per token");
+  TORCH_CHECK(key.stride(2) == 1 && key.stride(1) == 128 && value.stride(2) == 1 && value.stride(1) == 128,
+              "the [8, 128] part of each key / value row must be contiguous");
+  TORCH_CHECK(key_cache.dim() == 4 && key_cache.size(1) == 128 && key_cache.size(2) == 8 &&
+                  key_cache.size(3) == 128 && key_cache.is_contiguous(),
+              "key_cache must be a contiguous [pages, 128, 8, 128] tensor");
+  TORCH_CHECK(value_cache.sizes() == key_cache.sizes() && value_cache.is_contiguous(),
+              "value_cache must be contiguous with the shape of key_cache");
+  at::assert_no_overlap(key_cache, value_cache);
+  at::assert_no_overlap(key_cache, key);
+  at::assert_no_overlap(key_cache, value);
+  at::assert_no_overlap(value_cache, key);
+  at::assert_no_overlap(value_cache, value);
+  const int64_t num_tokens = key.size(0);
+  if (num_tokens == 0) return;
+  c10::OptionalDeviceGuard guard(key.device());
+  void* stream = c10::hip::getCurrentHIPStream(key.device().index()).stream();
+  const int status =
+      tm_reshape_and_cache(key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                           slot_mapping.data_ptr<int64_t>(), num_tokens, key.stride(0), value.stride(0),
+                           key_cache.size(0), stream);
+  check_status(status, "reshape_and_cache");
+}
+
+void meta_reshape_and_cache(const at::Tensor&, const at::Tensor&, at::Tensor&, at::Tensor&, const at::Tensor&) {}
+
 // Shape-only implementations (the reference's InferShape: out = query shape,
 // operator/op_host/triangle_paged_sparse_attention.cpp:332-346).
 at::Tensor meta_functional(const at::Tensor& query, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
@@ -218,16 +269,21 @@ TORCH_LIBRARY_FRAGMENT(trianglemix, ops) {
   ops.def(
       "dense_paged_causal_attention.out(Tensor query, Tensor key_cache, Tensor value_cache, "
       "Tensor block_table, int query_start, int seq_len, float scale, *, Tensor(a!) out) -> Tensor(a!)");
+  ops.def(
+      "reshape_and_cache(Tensor key, Tensor value, Tensor(a!) key_cache, Tensor(b!) value_cache, "
+      "Tensor slot_mapping) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(trianglemix, CUDA, ops) {
   ops.impl("triangle_paged_sparse_attention.out", &trianglemix_rocm::triangle_paged_sparse_attention_out);
   ops.impl("npu_triangle_paged_sparse_attention", &trianglemix_rocm::triangle_paged_sparse_attention_out);
   ops.impl("dense_paged_causal_attention.out", &trianglemix_rocm::dense_paged_causal_attention_out);
+  ops.impl("reshape_and_cache", &trianglemix_rocm::reshape_and_cache);
 }
 
 TORCH_LIBRARY_IMPL(trianglemix, Meta, ops) {
   ops.impl("triangle_paged_sparse_attention.out", &trianglemix_rocm::meta_out);
   ops.impl("npu_triangle_paged_sparse_attention", &trianglemix_rocm::meta_out);
   ops.impl("dense_paged_causal_attention.out", &trianglemix_rocm::meta_dense_out);
+  ops.impl("reshape_and_cache", &trianglemix_rocm::meta_reshape_and_cache);
 }

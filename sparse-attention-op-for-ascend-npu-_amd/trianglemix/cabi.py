@@ -80,3 +80,16 @@ def dense_paged_causal_attention(query, key_cache, value_cache, block_table, out
         query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(), out.data_ptr(),
         query.shape[0], key_cache.shape[0], block_table.shape[-1], query_start, seq_len,
         float(scale), ws_ptr, ws_bytes, st))
+
+
+def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, *, stream=None) -> None:
+    """Scatter key / value rows ``[T, 8, 128]`` (row-strided views allowed) into cache slots.
+
+    Token ``i`` goes to page ``slot_mapping[i] // 128``, offset ``slot_mapping[i] % 128``
+    (int64); negative slots are padding and are skipped.
+    """
+    lib = load_hip_library()
+    st = _stream(key, stream)
+    _check(lib.tm_reshape_and_cache(
+        key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.data_ptr(),
+        key.shape[0], key.stride(0), value.stride(0), key_cache.shape[0], st))

@@ -76,6 +76,8 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_float, vp, i64, vp]
     lib.tm_dense_paged_causal_attention_workspace_size.restype = i64
     lib.tm_dense_paged_causal_attention_workspace_size.argtypes = [i64, i64, i64]
+    lib.tm_reshape_and_cache.restype = ctypes.c_int
+    lib.tm_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, vp]
     del i32p
     return lib
 

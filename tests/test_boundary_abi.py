@@ -56,7 +56,8 @@ def test_header_functions_are_exported(lib):
     assert names == sorted([
         "tm_abi_version", "tm_status_string", "tm_last_error",
         "tm_triangle_paged_sparse_attention", "tm_triangle_paged_sparse_attention_workspace_size",
-        "tm_dense_paged_causal_attention", "tm_dense_paged_causal_attention_workspace_size"])
+        "tm_dense_paged_causal_attention", "tm_dense_paged_causal_attention_workspace_size",
+        "tm_reshape_and_cache"])
     raw = ctypes.CDLL(str(native.HIP_LIBRARY))
     for name in names:
         assert getattr(raw, name) is not None, name
@@ -125,6 +126,39 @@ def test_dense_entry_validation_errors(lib):
     assert r == 1
 
 
+KW_GOOD = dict(key=0x10000, value=0x20000, kc=0x1000000, vc=0x2000000, slots=0x3000, tokens=512, ks=1024, vs=1024,
+               pages=71)
+
+
+def _kv_write(lib, **over):
+    a = dict(KW_GOOD, **over)
+    return lib.tm_reshape_and_cache(a["key"], a["value"], a["kc"], a["vc"], a["slots"], a["tokens"], a["ks"],
+                                    a["vs"], a["pages"], None)
+
+
+@pytest.mark.parametrize("over,status,msg", [
+    (dict(tokens=-1), 1, "num_tokens"),
+    (dict(pages=0), 1, "pages > 0"),
+    (dict(pages=(1 << 22) + 1), 2, "limit is 4194304"),
+    (dict(key=None), 1, "non-null"),
+    (dict(slots=None), 1, "non-null"),
+    (dict(ks=1000), 1, "row stride"),
+    (dict(vs=1028), 1, "row stride"),
+    (dict(value=0x20004), 1, "16-byte aligned"),
+    (dict(vc=0x1000000 + 71 * 256 * 1024 - 16), 1, "must not overlap"),   # caches overlap
+    (dict(key=0x1000000 + 4096), 1, "must not overlap"),                  # source inside the key cache
+    (dict(slots=0x2000000 + 64), 1, "must not overlap"),                  # slot mapping inside the value cache
+])
+def test_kv_write_validation_errors(lib, over, status, msg):
+    assert _kv_write(lib, **over) == status
+    assert re.search(msg, lib.tm_last_error().decode()), lib.tm_last_error()
+
+
+def test_kv_write_without_tokens_enqueues_nothing(lib):
+    # no pointer is dereferenced and no HIP call is made for an empty chunk
+    assert _kv_write(lib, tokens=0, key=None, value=None, slots=None) == 0
+
+
 def test_workspace_sizes(lib):
     ws = lib.tm_triangle_paged_sparse_attention_workspace_size
     dws = lib.tm_dense_paged_causal_attention_workspace_size
@@ -172,6 +206,10 @@ def test_adapter_schemas_match_reference(adapter):
         assert str(schema) == schemas[name], name
     alias = str(adapter.trianglemix.npu_triangle_paged_sparse_attention.default._schema)
     assert "Tensor(a!) out) -> Tensor(a!)" in alias and "int prompt_len, float scale" in alias
+    # the paged KV write keeps vLLM's reshape_and_cache argument order (bf16 caches, no scales)
+    assert str(adapter.trianglemix.reshape_and_cache.default._schema) == (
+        "trianglemix::reshape_and_cache(Tensor key, Tensor value, Tensor(a!) key_cache, Tensor(b!) value_cache, "
+        "Tensor slot_mapping) -> ()")
 
 
 def test_adapter_load_is_idempotent_and_refuses_second_path(adapter, tmp_path):
@@ -203,3 +241,6 @@ def test_cpu_tensors_have_no_kernel(adapter):
                                                                  out=torch.empty_like(q))
     with pytest.raises(NotImplementedError):
         adapter.trianglemix_reference.dense_paged_causal_attention(q, k, k, bt, 0, 4, 0.088)
+    kv = torch.zeros(4, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        adapter.trianglemix.reshape_and_cache(kv, kv, k, k.clone(), torch.zeros(4, dtype=torch.int64))
