@@ -62,11 +62,13 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
 // ceil(n / T) near-equal items of at most T tiles; T is chosen by simulating
 // the greedy dispatch of the items (issued heaviest row block first) onto
 // kSlots slots, an item costing kItemFixedTiles + its tiles, and taking the T
-// with the shortest makespan (ties: larger T, fewer partials).  T is at least
+// with the shortest makespan (ties: larger T, fewer partials); a plan that
+// splits anything also pays for the combine kernel.  T is at least
 // kMinSplitTiles (1024 keys: a split's fp32 partial of 66 KB stays small next
 // to the K/V it reads, 16 KB per 32-key tile) and at most kMaxItemTiles.
 constexpr int kSlots = 16;
 constexpr int kItemFixedTiles = 15;  // start-up, merge and store of an item, in tile times (measured)
+constexpr int kCombineTiles = 15;    // the combine kernel a plan with splits adds, in tile times (measured)
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 // Beyond this many items per candidate the simulation is skipped (its host
 // cost would show): T then spreads the chunk's tiles over kSlots items.
@@ -85,8 +87,10 @@ int64_t simulated_makespan(const std::vector<int>& row_tiles, int T) {
     }
   }
   int64_t makespan = 0;
+  bool any_split = false;
   for (const int64_t f : slot) makespan = f > makespan ? f : makespan;
-  return makespan;
+  for (const int n : row_tiles) any_split = any_split || n > T;
+  return makespan + (any_split ? kCombineTiles : 0);
 }
 
 int choose_tiles_per_split(const std::vector<int>& row_tiles) {

@@ -6,12 +6,21 @@ precedence (``additional_config["trianglemix"]`` first, then the
 compatibility interface, then defaults) and strict boolean coercion
 (:16-29).  The environment names are kept verbatim so existing deployments
 switch without edits.
+
+One key is this build's own: ``gate_profile`` (environment
+``VLLM_ASCEND_TRIANGLE_MIX_GATE_PROFILE``) names a crossover profile measured
+by ``trianglemix.calibrate`` -- a name under ``trianglemix/gate_profiles/``
+(``"mi355x"`` ships) or a JSON path.  Its gates replace the defaults of the
+five ``direct_*`` gate keys; explicit keys and environment variables still
+win.  Unset, the reference's 910B-measured defaults apply unchanged.
 """
 
 from __future__ import annotations
 
+import json
 import os
 from dataclasses import dataclass
+from pathlib import Path
 from typing import Any, Mapping
 
 from .kernel import TriangleMixConfig, parse_layer_indices
@@ -80,13 +89,34 @@ _INT_KEYS = (
 )
 
 
+_GATE_FIELDS = ("direct_min_seq_len", "direct_min_sparse_rows", "direct_min_saved_qk",
+                "direct_split_min_sparse_rows", "direct_split_min_saved_qk")
+GATE_PROFILE_DIR = Path(__file__).resolve().parent / "gate_profiles"
+
+
+def load_gate_profile(name_or_path: str) -> dict[str, int]:
+    """The five ``direct_*`` gates of a calibration profile (a shipped name or a JSON path)."""
+    text = str(name_or_path).strip()
+    path = Path(text) if text.endswith(".json") else GATE_PROFILE_DIR / f"{text}.json"
+    if not path.is_file():
+        raise ValueError(f"TriangleMix gate_profile {name_or_path!r} not found ({path})")
+    gates = json.loads(path.read_text()).get("gates", {})
+    missing = [f for f in _GATE_FIELDS if f not in gates]
+    if missing:
+        raise ValueError(f"TriangleMix gate_profile {name_or_path!r} lacks {missing}")
+    return {f: int(gates[f]) for f in _GATE_FIELDS}
+
+
 def resolve_plugin_config(vllm_config: object | None) -> PluginConfig:
     """Resolve typed config, preferring ``additional_config.trianglemix``."""
     additional = _mapping(getattr(vllm_config, "additional_config", None))
     section = _mapping(additional.get("trianglemix", additional))
     layers = _value(section, "layers", _ENV + "LAYERS", "")
     layers_text = ",".join(str(x) for x in layers) if isinstance(layers, (list, tuple, set)) else str(layers)
-    ints = {field: int(_value(section, key, env, default)) for key, env, default, field in _INT_KEYS}
+    profile = str(_value(section, "gate_profile", _ENV + "GATE_PROFILE", "") or "")
+    profile_gates = load_gate_profile(profile) if profile else {}
+    ints = {field: int(_value(section, key, env, profile_gates.get(field, default)))
+            for key, env, default, field in _INT_KEYS}
     kernel = TriangleMixConfig(
         enabled=_coerce_bool(_value(section, "enabled", "VLLM_ASCEND_ENABLE_TRIANGLE_MIX", False), name="enabled"),
         layer_indices=parse_layer_indices(layers_text),
