@@ -83,6 +83,8 @@
 // split partials merge with the same rescale rule.
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 #include "trianglemix_kernel.h"
@@ -591,31 +593,44 @@ triangle_paged_attention_kernel(KernelParams p) {
   // ---- merge the four KV quarters through LDS ----
   // Quarter kq keeps d-block kq and hands its three other d-blocks to their
   // owners.  Given block index gi (0..2 among the blocks a quarter gives away)
-  // selects the slot: xo_gi[hl][quarter][v][lane] lives in k_lds0, k_lds1,
-  // v_lds0 for gi = 0, 1, 2; xm / xl [hl][quarter][lane] live in v_lds1.
+  // selects the slot: xo_gi[hl][quarter][v/4][lane][4] lives in k_lds0,
+  // k_lds1, v_lds0 for gi = 0, 1, 2 (16-byte accesses, one 1 KB stretch per
+  // instruction); xm / xl [hl][quarter][lane] live in v_lds1.  kq is
+  // wave-uniform, so one scalar switch picks a variant with every block and
+  // slot index fixed at compile time; both barriers stay outside the
+  // switches.
   wait_dma();
   __syncthreads();  // all compute and every (empty) prefetch done; the slots are free
   static_assert(kHeadsPerGroup * kQuarters * 16 * 64 * 4 == kSlotBytes, "one given block fills one slot");
   auto xo = [&](int gi) {
-    return reinterpret_cast<float*>(gi == 0 ? k_lds0 : (gi == 1 ? k_lds1 : v_lds0));
+    return reinterpret_cast<f32x4_t*>(gi == 0 ? k_lds0 : (gi == 1 ? k_lds1 : v_lds0));
   };
   float* xm = reinterpret_cast<float*>(v_lds1);
   float* xl = xm + kHeadsPerGroup * kQuarters * 64;
   const int self = hl * kQuarters + kq;
+  auto give = [&](auto kq_c) {
+    constexpr int KQ = decltype(kq_c)::value;
 #pragma unroll
-  for (int m = 0; m < kHeadDim / 32; ++m) {
-    if (m == kq) continue;
-    const int gi = m < kq ? m : m - 1;  // index of block m among those this quarter gives away
-    float* dst = xo(gi) + self * 16 * 64 + lane;
+    for (int m = 0; m < kHeadDim / 32; ++m) {
+      if (m == KQ) continue;
+      const int gi = m < KQ ? m : m - 1;  // index of block m among those this quarter gives away
+      f32x4_t* dst = xo(gi) + self * 4 * 64 + lane;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) dst[v * 64] = o_acc[m][v];
+      for (int g = 0; g < 4; ++g) {
+        dst[g * 64] = f32x4_t{o_acc[m][4 * g], o_acc[m][4 * g + 1], o_acc[m][4 * g + 2], o_acc[m][4 * g + 3]};
+      }
+    }
+  };
+  switch (kq) {
+    case 0: give(std::integral_constant<int, 0>{}); break;
+    case 1: give(std::integral_constant<int, 1>{}); break;
+    case 2: give(std::integral_constant<int, 2>{}); break;
+    default: give(std::integral_constant<int, 3>{}); break;
   }
   xm[self * 64 + lane] = m_run;
   xl[self * 64 + lane] = l_run;
   __syncthreads();
-  f32x16_t kept = o_acc[0];
-#pragma unroll
-  for (int m = 1; m < kHeadDim / 32; ++m) kept = m == kq ? o_acc[m] : kept;
+  f32x16_t kept;
   {
     float mq[kQuarters], lq[kQuarters];
     float mt = -INFINITY;
@@ -627,18 +642,32 @@ triangle_paged_attention_kernel(KernelParams p) {
     }
     const float mu = mt == -INFINITY ? 0.0f : mt;
     float lt = 0.0f;
-    f32x16_t acc = kept * __builtin_amdgcn_exp2f(m_run - mu);
 #pragma unroll
-    for (int r = 0; r < kQuarters; ++r) {
-      const float a = __builtin_amdgcn_exp2f(mq[r] - mu);
-      lt += lq[r] * a;
-      if (r == kq) continue;
-      const int gi = kq < r ? kq : kq - 1;  // index of block kq among those quarter r gives away
-      const float* src = xo(gi) + (hl * kQuarters + r) * 16 * 64 + lane;
+    for (int r = 0; r < kQuarters; ++r) lt += lq[r] * __builtin_amdgcn_exp2f(mq[r] - mu);
+    auto gather = [&](auto kq_c) {
+      constexpr int KQ = decltype(kq_c)::value;
+      f32x16_t acc = o_acc[KQ] * __builtin_amdgcn_exp2f(m_run - mu);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[v] += src[v * 64] * a;
+      for (int r = 0; r < kQuarters; ++r) {
+        if (r == KQ) continue;
+        const float a = __builtin_amdgcn_exp2f(mq[r] - mu);
+        const int gi = KQ < r ? KQ : KQ - 1;  // index of block KQ among those quarter r gives away
+        const f32x4_t* src = xo(gi) + (hl * kQuarters + r) * 4 * 64 + lane;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4_t x = src[g * 64];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[4 * g + e] += x[e] * a;
+        }
+      }
+      return acc;
+    };
+    switch (kq) {
+      case 0: kept = gather(std::integral_constant<int, 0>{}); break;
+      case 1: kept = gather(std::integral_constant<int, 1>{}); break;
+      case 2: kept = gather(std::integral_constant<int, 2>{}); break;
+      default: kept = gather(std::integral_constant<int, 3>{}); break;
     }
-    kept = acc;
     l_run = lt;
     m_run = mt;
   }
