@@ -25,6 +25,16 @@ Reported JSON line (rank 0 only):
   chunks, median of 2 passes after a warm-up, on this host's cores.
 
 ``--gpus N`` with N > 1 is refused: this build runs on one GPU.
+
+Other workloads (not the headline line; one JSON line each):
+
+* ``--workload config3`` -- L=8320 in chunks of 2048 with 1 % of the K
+  entries set to +-8 (the same legs as above);
+* ``--workload config4`` -- long-context curve, chunk 2048: the whole prefill
+  as one HIP graph, sparse vs dense, for L from 1024 to 131072, and the
+  crossover L;
+* ``--workload config5`` -- 36 layers of config 2 through the plan / router
+  layer (layers 5, 7, 10, 15-35 sparse), eager, with the counter snapshot.
 """
 
 from __future__ import annotations
@@ -60,6 +70,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--only", choices=("sparse", "dense"), help="run one kernel only (for profiling)")
+    ap.add_argument("--workload", choices=("config2", "config3", "config4", "config5"), default="config2")
+    ap.add_argument("--outliers", type=float, default=None, help="fraction of K entries set to +-8")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run 5 plain device copies of MIB MiB (scales rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
@@ -78,13 +90,21 @@ def main() -> int:
     from trianglemix.workload import (SCALE, chunk_bytes, chunk_flops, executed_flops, kv_bytes, make_cache,
                                       make_query, prompt_chunks)
 
+    if args.workload == "config4":
+        return config4_curve(args)
+    if args.workload == "config5":
+        return config5_stack(args)
+    headline = args.workload == "config2" and args.prompt == 8192 and args.chunk == 512 and not args.outliers
+    if args.workload == "config3":
+        args.prompt, args.chunk = 8320, 2048
+        args.outliers = 0.01 if args.outliers is None else args.outliers
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     native.load_hip_library()
     native.load_triangle_mix_adapter()
     dev = torch.device("cuda:0")
     chunks = prompt_chunks(args.prompt, args.chunk)
 
-    k, v, bt = make_cache(args.prompt, args.seed, std=1.0)
+    k, v, bt = make_cache(args.prompt, args.seed, std=1.0, outlier_frac=args.outliers or 0.0)
     qfull = make_query(args.prompt, args.seed + 1, std=1.0)
     kd, vd, btd = k.to(dev), v.to(dev), bt.to(dev)
     qs = [qfull[c.query_start:c.seq_len].contiguous().to(dev) for c in chunks]
@@ -193,16 +213,21 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    traffic = read_traffic_summary()
+    traffic = read_traffic_summary() if headline else None
 
-    kv_write = kv_write_bench(args, chunks, k, v, bt, dev) if args.only is None else None
+    kv_write = kv_write_bench(args, chunks, k, v, bt, dev) if args.only is None and headline else None
 
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
         cpu = cpu_baseline(chunks, qfull, k, v, bt, SCALE)
 
+    workload = (f"config2: one request, L={args.prompt}, chunked prefill {args.chunk} x {n} chunks, "
+                "Hq=32 Hkv=8 D=128 page=128, one layer")
+    if args.workload == "config3":
+        workload = (f"config3: one request, L={args.prompt}, chunked prefill {args.chunk} x {n} chunks, "
+                    f"{args.outliers:.0%} of K entries +-8, Hq=32 Hkv=8 D=128 page=128, one layer")
     line = {
-        "metric": METRIC,
+        "metric": METRIC if headline else f"sparse-prefill attn µs/chunk + MFMA %peak ({args.workload})",
         "value": round(us_per_chunk, 3),
         "unit": "us/chunk",
         "n_gpus": 1,
@@ -215,9 +240,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 Q/K/V, random page table)",
         "config": {
-            "workload": f"config2: one request, L={args.prompt}, chunked prefill {args.chunk} x {n} chunks, "
-                        "Hq=32 Hkv=8 D=128 page=128, one layer",
-            "timing": "HIP-graph replay of the 16 launches" if not args.no_graph else "eager launches",
+            "workload": workload,
+            "timing": f"HIP-graph replay of the {n} launches" if not args.no_graph else "eager launches",
         },
         "roofline": {
             "bound": "mfma",
@@ -240,6 +264,187 @@ def main() -> int:
         },
         "kv_write": kv_write,
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def graph_of(step):
+    """HIP graph of ``step`` (captured after one eager warm-up on the capture stream)."""
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    return graph
+
+
+def median_ms(run, reps: int, windows: int = 3) -> float:
+    """Median over ``windows`` of the mean time of ``reps`` back-to-back calls (ms per call)."""
+    import torch
+
+    times = []
+    for _ in range(windows):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            run()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e) / reps)
+    return statistics.median(times)
+
+
+def config4_curve(args) -> int:
+    """Long-context curve (chunk 2048): whole-prefill sparse vs dense attention time per L, and the crossover."""
+    import torch
+
+    from trianglemix import native
+    from trianglemix.workload import SCALE, chunk_flops, prompt_chunks
+
+    native.load_hip_library()
+    native.load_triangle_mix_adapter()
+    dev = torch.device("cuda:0")
+    sparse_op = torch.ops.trianglemix.triangle_paged_sparse_attention.out
+    dense_op = torch.ops.trianglemix.dense_paged_causal_attention.out
+    chunk = 2048
+    curve = []
+    for L in (1024, 2048, 4096, 8192, 16384, 32768, 131072):
+        g = torch.Generator(device=dev).manual_seed(args.seed + L)
+        logical = (L + 127) // 128
+        pages = logical + 7
+        table = torch.randperm(pages, generator=g, device=dev)[:logical].to(torch.int32).view(1, -1)
+        kc = torch.randn(pages, 128, 8, 128, generator=g, device=dev, dtype=torch.bfloat16)
+        vc = torch.randn(pages, 128, 8, 128, generator=g, device=dev, dtype=torch.bfloat16)
+        q = torch.randn(L, 32, 128, generator=g, device=dev, dtype=torch.bfloat16)
+        out = torch.empty_like(q)
+        chunks = prompt_chunks(L, chunk)
+
+        def sparse_step():
+            for c in chunks:
+                sparse_op(q[c.query_start:c.seq_len], kc, vc, table, c.query_start, c.seq_len, L, SCALE,
+                          out=out[c.query_start:c.seq_len])
+
+        def dense_step():
+            for c in chunks:
+                dense_op(q[c.query_start:c.seq_len], kc, vc, table, c.query_start, c.seq_len, SCALE,
+                         out=out[c.query_start:c.seq_len])
+
+        gs, gd = graph_of(sparse_step), graph_of(dense_step)
+        reps = 2 if L >= 131072 else (5 if L >= 32768 else 20)
+        ms_s = statistics.mean([median_ms(gs.replay, reps), median_ms(gs.replay, reps)])  # A B B A
+        ms_d = statistics.mean([median_ms(gd.replay, reps), median_ms(gd.replay, reps)])
+        fs = sum(chunk_flops(c) for c in chunks)
+        fd = sum(chunk_flops(c, dense=True) for c in chunks)
+        curve.append({"L": L, "chunks": len(chunks), "sparse_ms": round(ms_s, 4), "dense_ms": round(ms_d, 4),
+                      "speedup": round(ms_d / ms_s, 3), "sparse_gflop": round(fs / 1e9, 2),
+                      "dense_gflop": round(fd / 1e9, 2), "sparse_tflops": round(fs / (ms_s * 1e-3) / 1e12, 1),
+                      "dense_tflops": round(fd / (ms_d * 1e-3) / 1e12, 1)})
+        print(f"# config4 L={L}: sparse {ms_s:.3f} ms dense {ms_d:.3f} ms x{ms_d / ms_s:.2f}", file=sys.stderr,
+              flush=True)
+        del kc, vc, q, out, gs, gd
+        torch.cuda.empty_cache()
+    wins = [p["L"] for p in curve if p["sparse_ms"] < p["dense_ms"]]
+    line = {
+        "metric": "long-context prefill attention, sparse vs dense (config4, chunk 2048)",
+        "value": next(p["sparse_ms"] for p in curve if p["L"] == 32768),
+        "unit": "ms/prefill at L=32768",
+        "n_gpus": 1,
+        "higher_is_better": False,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V from the GPU generator, random page table)",
+        "config": {"workload": "config4: one request per L, chunked prefill of 2048, Hq=32 Hkv=8 D=128 page=128, "
+                               "one layer; each prefill is one HIP graph of its chunk launches"},
+        "curve": curve,
+        "crossover_L": min(wins) if wins else None,
+        "crossover_note": "smallest measured L whose whole sparse prefill beats the dense one; L=1024 is one "
+                          "1024-row chunk, whose one-kernel graph replay is dominated by the graph launch (the "
+                          "eager crossover sweep of trianglemix.calibrate measures that chunk at x1.02)",
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def config5_stack(args) -> int:
+    """36 layers x config 2 through the plan / router layer; counters from the stats snapshot."""
+    import torch
+
+    from trianglemix import native
+    from trianglemix.config import resolve_plugin_config
+    from trianglemix.planning import build_batch_plan
+    from trianglemix.router import TriangleMixRouter
+    from trianglemix.stats import TriangleMixRuntimeStats
+    from trianglemix.workload import SCALE, chunk_flops, prompt_chunks
+
+    native.load_hip_library()
+    native.load_triangle_mix_adapter()
+    dev = torch.device("cuda:0")
+    L, chunk, layers = 8192, 512, 36
+    selected = "5,7,10,15-35"
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    logical = L // 128
+    pages = logical + 7
+    table = torch.randperm(pages, generator=g, device=dev)[:logical].to(torch.int32).view(1, -1)
+    kcs = [torch.randn(pages, 128, 8, 128, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    vcs = [torch.randn(pages, 128, 8, 128, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    qs = [torch.randn(L, 32, 128, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    outs = [torch.empty_like(x) for x in qs]
+    chunks = prompt_chunks(L, chunk)
+
+    class _Vllm:
+        def __init__(self, enabled):
+            self.additional_config = {"trianglemix": {"enabled": enabled, "layers": selected}}
+
+    def run_prefill(router, cfg):
+        for c in chunks:
+            plan = build_batch_plan(state_name="ChunkedPrefill", cumulative_query_ends=[c.query_tokens],
+                                    seq_lens=[c.seq_len], prompt_lens=[L], num_decodes=0, num_prefills=1,
+                                    config=cfg.kernel)
+            for i in range(layers):
+                router.prefill_attention(layer_name=f"model.layers.{i}.self_attn.attn", plan=plan,
+                                         query=qs[i][c.query_start:c.seq_len], key_cache=kcs[i], value_cache=vcs[i],
+                                         block_table=table, output=outs[i][c.query_start:c.seq_len],
+                                         softmax_scale=SCALE)
+
+    results = {}
+    for name, enabled in (("trianglemix", True), ("all_dense", False)):
+        cfg = resolve_plugin_config(_Vllm(enabled))
+        stats = TriangleMixRuntimeStats()
+        router = TriangleMixRouter(cfg, stats=stats)
+        run_prefill(router, cfg)  # warm-up
+        torch.cuda.synchronize()
+        stats.snapshot(reset=True)
+        ms = median_ms(lambda: run_prefill(router, cfg), 1)
+        snap = stats.snapshot(reset=False)
+        results[name] = {"ms_per_prefill": round(ms, 3), "stats": snap}
+    sel = resolve_plugin_config(_Vllm(True)).kernel.layer_indices
+    gflop = sum(chunk_flops(c, dense=(i not in sel)) for c in chunks for i in range(layers)) / 1e9
+    dense_gflop = sum(chunk_flops(c, dense=True) for c in chunks) * layers / 1e9
+    tm = results["trianglemix"]["stats"]
+    line = {
+        "metric": "36-layer prefill attention through the plan / router layer (config5)",
+        "value": results["trianglemix"]["ms_per_prefill"],
+        "unit": "ms/prefill (36 layers x 16 chunks, eager)",
+        "n_gpus": 1,
+        "higher_is_better": False,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V per layer from the GPU generator, random page table)",
+        "config": {"workload": f"config5: L={L}, chunked prefill {chunk} x {len(chunks)}, {layers} layers, "
+                               f"layers {selected} sparse", "gates": "reference defaults"},
+        "all_dense_ms_per_prefill": results["all_dense"]["ms_per_prefill"],
+        "attention_time_cut": round(1 - results["trianglemix"]["ms_per_prefill"]
+                                    / results["all_dense"]["ms_per_prefill"], 4),
+        "gflop": {"routed": round(gflop, 1), "all_dense": round(dense_gflop, 1)},
+        "counters": tm["counters"],
+        "fallback_reasons": tm["fallback_reasons"],
+        "routing": tm["performance"],
     }
     print(json.dumps(line), flush=True)
     return 0

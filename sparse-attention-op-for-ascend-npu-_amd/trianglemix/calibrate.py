@@ -168,7 +168,7 @@ def measure(lengths, chunk_sizes, reps: int, seed: int, log=print):
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--lengths", default="2048,4096,8192,16384")
+    ap.add_argument("--lengths", default="1024,2048,4096,8192,16384")
     ap.add_argument("--chunks", default="256,512,1024,2048")
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--margin", type=float, default=0.05,
