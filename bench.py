@@ -399,8 +399,11 @@ def config5_stack(args) -> int:
     chunks = prompt_chunks(L, chunk)
 
     class _Vllm:
-        def __init__(self, enabled):
-            self.additional_config = {"trianglemix": {"enabled": enabled, "layers": selected}}
+        def __init__(self, enabled, profile=""):
+            section = {"enabled": enabled, "layers": selected}
+            if profile:
+                section["gate_profile"] = profile
+            self.additional_config = {"trianglemix": section}
 
     def run_prefill(router, cfg):
         for c in chunks:
@@ -414,8 +417,9 @@ def config5_stack(args) -> int:
                                          softmax_scale=SCALE)
 
     results = {}
-    for name, enabled in (("trianglemix", True), ("all_dense", False)):
-        cfg = resolve_plugin_config(_Vllm(enabled))
+    for name, enabled, profile in (("trianglemix", True, ""), ("trianglemix_mi355x_gates", True, "mi355x"),
+                                   ("all_dense", False, "")):
+        cfg = resolve_plugin_config(_Vllm(enabled, profile))
         stats = TriangleMixRuntimeStats()
         router = TriangleMixRouter(cfg, stats=stats)
         run_prefill(router, cfg)  # warm-up
@@ -439,6 +443,13 @@ def config5_stack(args) -> int:
         "config": {"workload": f"config5: L={L}, chunked prefill {chunk} x {len(chunks)}, {layers} layers, "
                                f"layers {selected} sparse", "gates": "reference defaults"},
         "all_dense_ms_per_prefill": results["all_dense"]["ms_per_prefill"],
+        "mi355x_gates": {
+            "ms_per_prefill": results["trianglemix_mi355x_gates"]["ms_per_prefill"],
+            "attention_time_cut": round(1 - results["trianglemix_mi355x_gates"]["ms_per_prefill"]
+                                        / results["all_dense"]["ms_per_prefill"], 4),
+            "counters": results["trianglemix_mi355x_gates"]["stats"]["counters"],
+            "fallback_reasons": results["trianglemix_mi355x_gates"]["stats"]["fallback_reasons"],
+        },
         "attention_time_cut": round(1 - results["trianglemix"]["ms_per_prefill"]
                                     / results["all_dense"]["ms_per_prefill"], 4),
         "gflop": {"routed": round(gflop, 1), "all_dense": round(dense_gflop, 1)},
