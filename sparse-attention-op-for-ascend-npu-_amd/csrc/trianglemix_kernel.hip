@@ -36,7 +36,8 @@
 // tile of iteration i, then the PV MFMAs of tile i interleaved with the mask
 // and row max of tile i+1 (the interleave is fixed in program order with
 // scheduling barriers).  LDS holds two K slots and two V slots, each with the
-// four tiles (one per quarter) of one iteration; the DMA of K for iteration
+// four tiles (one per quarter) of one iteration, plus the workgroup's Q (DMA'd
+// once, read into registers in the prologue); the DMA of K for iteration
 // i+2 (waves 0-3) and of V for iteration i+1 (waves 4-7) is spread over the
 // MFMA steps of iteration i, one instruction per step.  The four slots are
 // distinct LDS objects and the loop is unrolled by two so every access names
@@ -223,7 +224,9 @@ __device__ __forceinline__ void mask_window(f32x16_t& s, int thr, int thr_sink) 
 // log2 units) updates the row state and rescales O when needed.  Returns the
 // exponent shift of the tile's exponentials.
 __device__ __forceinline__ float softmax_update(float m_tile, float& m_run, float& l_run, f32x16_t* o_acc) {
-  if (__any(m_tile > m_run + kLazyRescale)) {  // wave-uniform branch; always taken on a row's first keys
+  // Wave-uniform branch, taken when some row's max grows past the lazy bound
+  // (or a row meets its first attended keys after an all-masked first tile).
+  if (__any(m_tile > m_run + kLazyRescale)) {
     const float m_new = fmaxf(m_run, m_tile);
     // exp2(-inf - x) = 0 rescales an empty state; a row still without keys keeps m = -inf.
     const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
