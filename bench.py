@@ -41,6 +41,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import logging
 import os
 import statistics
 import sys
@@ -378,6 +379,8 @@ def config5_stack(args) -> int:
 
     from trianglemix import native
     from trianglemix.config import resolve_plugin_config
+    from trianglemix.counters import aggregate as counters_aggregate
+    from trianglemix.counters import report_status, scan_events
     from trianglemix.planning import build_batch_plan
     from trianglemix.router import TriangleMixRouter
     from trianglemix.stats import TriangleMixRuntimeStats
@@ -399,11 +402,19 @@ def config5_stack(args) -> int:
     chunks = prompt_chunks(L, chunk)
 
     class _Vllm:
-        def __init__(self, enabled, profile=""):
-            section = {"enabled": enabled, "layers": selected}
+        def __init__(self, enabled, profile="", log_interval=0):
+            section = {"enabled": enabled, "layers": selected, "stats_log_interval": log_interval}
             if profile:
                 section["gate_profile"] = profile
             self.additional_config = {"trianglemix": section}
+
+    class _Lines(logging.Handler):
+        def __init__(self):
+            super().__init__()
+            self.lines = []
+
+        def emit(self, record):
+            self.lines.append(record.getMessage())
 
     def run_prefill(router, cfg):
         for c in chunks:
@@ -417,17 +428,40 @@ def config5_stack(args) -> int:
                                          softmax_scale=SCALE)
 
     results = {}
-    for name, enabled, profile in (("trianglemix", True, ""), ("trianglemix_mi355x_gates", True, "mi355x"),
-                                   ("all_dense", False, "")):
-        cfg = resolve_plugin_config(_Vllm(enabled, profile))
+    router_log = logging.getLogger("trianglemix.router")
+    for name, enabled, profile, interval in (("trianglemix", True, "", 0),
+                                             ("trianglemix_mi355x_gates", True, "mi355x", 0),
+                                             ("all_dense", False, "", 0),
+                                             ("trianglemix_logged", True, "", len(chunks))):
+        cfg = resolve_plugin_config(_Vllm(enabled, profile, interval))
         stats = TriangleMixRuntimeStats()
         router = TriangleMixRouter(cfg, stats=stats)
         run_prefill(router, cfg)  # warm-up
         torch.cuda.synchronize()
         stats.snapshot(reset=True)
-        ms = median_ms(lambda: run_prefill(router, cfg), 1)
+        handler = _Lines()
+        router_log.addHandler(handler)
+        level = router_log.level
+        router_log.setLevel(logging.INFO)
+        try:
+            ms = median_ms(lambda: run_prefill(router, cfg), 1)
+        finally:
+            router_log.removeHandler(handler)
+            router_log.setLevel(level)
         snap = stats.snapshot(reset=False)
-        results[name] = {"ms_per_prefill": round(ms, 3), "stats": snap}
+        results[name] = {"ms_per_prefill": round(ms, 3), "stats": snap, "log_lines": handler.lines}
+    # the structured log of the logged run, aggregated the way a run's worker logs are
+    logged = results["trianglemix_logged"]
+    report = counters_aggregate(scan_events("\n".join(logged["log_lines"]), source="config5"))
+    structured_log = {
+        "stats_log_interval": len(chunks),
+        "events": report["event_count"],
+        "status": report_status(report),
+        "aggregate_equals_snapshot": (report["aggregate"]["counters"] == logged["stats"]["counters"]
+                                      and report["aggregate"]["layers"] == logged["stats"]["layers"]),
+        "ms_per_prefill": logged["ms_per_prefill"],
+        "logging_overhead": round(logged["ms_per_prefill"] / results["trianglemix"]["ms_per_prefill"] - 1, 4),
+    }
     sel = resolve_plugin_config(_Vllm(True)).kernel.layer_indices
     gflop = sum(chunk_flops(c, dense=(i not in sel)) for c in chunks for i in range(layers)) / 1e9
     dense_gflop = sum(chunk_flops(c, dense=True) for c in chunks) * layers / 1e9
@@ -456,6 +490,7 @@ def config5_stack(args) -> int:
         "counters": tm["counters"],
         "fallback_reasons": tm["fallback_reasons"],
         "routing": tm["performance"],
+        "structured_log": structured_log,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -19,7 +19,6 @@ strict mode, else it falls back with ``DIRECT_LAUNCH_ERROR``.
 
 from __future__ import annotations
 
-import json
 import logging
 import math
 import time
@@ -27,6 +26,7 @@ from dataclasses import dataclass
 from typing import Any, Callable
 
 from .config import PluginConfig
+from .counters import log_if_due
 from .kernel import (
     SUPPORTED_CACHE_BLOCK_SIZE,
     SUPPORTED_HEAD_SIZE,
@@ -169,9 +169,7 @@ class TriangleMixRouter:
                            seq_len=seq_len, output=view, softmax_scale=scale)
 
     def _log_if_due(self) -> None:
-        payload = self.stats.structured_log_if_due()
-        if payload is not None:
-            logger.info("%s", json.dumps(payload, sort_keys=True))
+        log_if_due(self.stats, logger)
 
     def _fallback(self, plan: TriangleBatchPlan, layer_index: int | None, reason: FallbackReason) -> None:
         # Graph-capture metadata is a reusable dummy, not a scheduled request.
