@@ -373,6 +373,129 @@ def config4_curve(args) -> int:
     return 0
 
 
+def _stand_in_vllm(prompt_len: int):
+    """A stand-in vLLM v1 Triton backend and GPU model runner with the signatures the seam allowlists.
+
+    Its own forward does what vLLM's Triton path does for a prefill chunk:
+    write the step's K/V into the paged cache, then attend -- here with the
+    gfx950 KV write and the dense companion kernel.  No vLLM is installed on
+    these machines; the stand-in lets the seam run a whole engine step loop.
+    """
+    import types
+
+    import torch
+
+    class Metadata:
+        def __init__(self, common):
+            self.num_actual_tokens = int(common.query_start_loc_cpu[-1])
+            self.seq_len = int(common.seq_lens_cpu[0])
+            self.block_table = common.block_table_tensor
+            self.slot_mapping = common.slot_mapping
+            self.causal = True
+            self.use_cascade = False
+
+    class TritonAttentionMetadataBuilder:
+        def __init__(self, kv_cache_spec, layer_names, vllm_config, device):
+            self.vllm_config = vllm_config
+
+        def build(self, common_prefix_len, common_attn_metadata, fast_build=False):
+            return Metadata(common_attn_metadata)
+
+        def build_for_cudagraph_capture(self, common_attn_metadata):
+            return self.build(0, common_attn_metadata)
+
+    class TritonAttentionImpl:
+        def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes, sliding_window, kv_cache_dtype,
+                     logits_soft_cap=None, attn_type="decoder", kv_sharing_target_layer_name=None, sinks=None):
+            self.num_heads, self.head_size, self.scale, self.num_kv_heads = num_heads, head_size, scale, num_kv_heads
+            self.alibi_slopes, self.sinks, self.logits_soft_cap = alibi_slopes, sinks, logits_soft_cap
+            self.sliding_window = (-1, -1)
+            self.kv_cache_dtype, self.attn_type = kv_cache_dtype, attn_type
+            self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
+
+        def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None, output_scale=None,
+                    output_block_scale=None):
+            kc, vc = kv_cache.unbind(0)
+            n, seq = attn_metadata.num_actual_tokens, attn_metadata.seq_len
+            torch.ops.trianglemix.reshape_and_cache(key[:n], value[:n], kc, vc, attn_metadata.slot_mapping[:n])
+            torch.ops.trianglemix.dense_paged_causal_attention.out(
+                query[:n], kc, vc, attn_metadata.block_table, seq - n, seq, self.scale, out=output[:n])
+            return output
+
+    class GPUModelRunner:
+        def __init__(self, builder):
+            self.builder = builder
+            self.input_batch = types.SimpleNamespace(num_reqs=1, num_prompt_tokens=[prompt_len])
+            self.speculative_config = None
+
+        def _prepare_inputs(self, scheduler_output):
+            return {"layers": self.builder.build(0, scheduler_output)}, None
+
+    backend = types.SimpleNamespace(TritonAttentionMetadataBuilder=TritonAttentionMetadataBuilder,
+                                    TritonAttentionImpl=TritonAttentionImpl,
+                                    get_tensor_model_parallel_world_size=lambda: 1)
+    return backend, types.SimpleNamespace(GPUModelRunner=GPUModelRunner)
+
+
+def vllm_seam_stack(qs, kcs, vcs, table, chunks, selected: str, prompt_len: int) -> dict:
+    """The config-5 stack through the vLLM-ROCm seam on a stand-in backend: ms/prefill with the seam routing
+    the selected layers, and with the feature off (every layer on the stand-in's own path); both write every
+    chunk's K/V, as an engine does."""
+    import types
+
+    import torch
+
+    from trianglemix import vllm_rocm
+    from trianglemix.cache import chunk_slot_mapping
+    from trianglemix.stats import runtime_stats
+    from trianglemix.workload import SCALE
+
+    backend, runner_mod = _stand_in_vllm(prompt_len)
+    vllm_rocm.patch_modules(backend, runner_mod)
+    layers = len(qs)
+    rows = torch.arange(prompt_len, device=table.device)
+    slots = table[0].long()[rows // 128] * 128 + rows % 128
+    # fresh K/V of every token: the values already in the cache, so every run attends the same data
+    kv = [(k.view(-1, 8, 128)[slots].contiguous(), v.view(-1, 8, 128)[slots].contiguous()) for k, v in zip(kcs, vcs)]
+    caches = [torch.stack([k, v]) for k, v in zip(kcs, vcs)]
+    outs = [torch.empty_like(q) for q in qs]
+    commons = [types.SimpleNamespace(
+        query_start_loc_cpu=torch.tensor([0, c.query_tokens], dtype=torch.int32),
+        seq_lens_cpu=torch.tensor([c.seq_len], dtype=torch.int32), num_reqs=1, causal=True,
+        block_table_tensor=table, slot_mapping=chunk_slot_mapping(table, c.query_start, c.query_tokens))
+        for c in chunks]
+    names = [types.SimpleNamespace(layer_name=f"model.layers.{i}.self_attn.attn") for i in range(layers)]
+    result = {}
+    for name, enabled in (("seam", True), ("seam_feature_off", False)):
+        cfg = types.SimpleNamespace(additional_config={"trianglemix": {"enabled": enabled, "layers": selected}})
+        builder = backend.TritonAttentionMetadataBuilder(None, [], cfg, table.device)
+        runner = runner_mod.GPUModelRunner(builder)
+        impls = [backend.TritonAttentionImpl(32, 128, SCALE, 8, None, None, "auto") for _ in range(layers)]
+
+        def prefill():
+            for c, common in zip(chunks, commons):
+                md = runner._prepare_inputs(common)[0]["layers"]
+                sl = slice(c.query_start, c.seq_len)
+                for i in range(layers):
+                    impls[i].forward(names[i], qs[i][sl], kv[i][0][sl], kv[i][1][sl], caches[i], md, outs[i][sl])
+
+        prefill()  # warm-up
+        torch.cuda.synchronize()
+        runtime_stats().snapshot(reset=True)
+        ms = median_ms(prefill, 1)
+        counters = runtime_stats().snapshot()["counters"]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        prefill()  # host time to issue one prefill (the GPU drains behind it)
+        host_ms = (time.perf_counter() - t0) * 1e3
+        torch.cuda.synchronize()
+        result[name] = {"ms_per_prefill": round(ms, 3), "host_issue_ms_per_prefill": round(host_ms, 3),
+                        "single_launch": counters.get("single_launch", 0), "layer_fia": counters.get("layer_fia", 0)}
+    result["attention_time_cut"] = round(1 - result["seam"]["ms_per_prefill"]
+                                         / result["seam_feature_off"]["ms_per_prefill"], 4)
+    return result
+
+
 def config5_stack(args) -> int:
     """36 layers x config 2 through the plan / router layer; counters from the stats snapshot."""
     import torch
@@ -491,6 +614,7 @@ def config5_stack(args) -> int:
         "fallback_reasons": tm["fallback_reasons"],
         "routing": tm["performance"],
         "structured_log": structured_log,
+        "vllm_seam": vllm_seam_stack(qs, kcs, vcs, table, chunks, selected, L),
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -7,8 +7,9 @@ ABI in ``include/trianglemix.h``) and ``_trianglemix_torch.so`` (the
 Modules mirror the reference's plugin package ``vllm_ascend_trianglemix``:
 ``kernel`` (op wrapper, span math), ``planning`` (per-step plan, fallback
 reasons), ``config``, ``stats`` (counters), ``native`` (library bootstrap),
-plus ``router`` (per-layer routing), ``counters`` (structured counter log
-and its run aggregator), ``cache`` (paged KV write), ``calibrate``
+plus ``router`` (per-layer routing), ``vllm_rocm`` (the vLLM-ROCm seam:
+``register`` patches vLLM v1's Triton attention backend), ``counters``
+(structured counter log and its run aggregator), ``cache`` (paged KV write), ``calibrate``
 (crossover gates), ``cabi`` (C ABI binding) and ``workload`` (seeded
 synthetic chunks, work accounting).
 """

@@ -20,6 +20,7 @@ ops exist only for ROCm device tensors and the native adapter must be loaded.
 
 from __future__ import annotations
 
+import functools
 import math
 import re
 from dataclasses import dataclass
@@ -118,8 +119,10 @@ class TriangleSparseSpan:
 _LAYER_RE = re.compile(r"(?:^|\.)layers\.(\d+)(?:\.|$)")
 
 
+@functools.lru_cache(maxsize=4096)
 def extract_layer_index(layer_name: str) -> int | None:
-    """Transformer layer index of a vLLM layer name (``model.layers.7.attn``)."""
+    """Transformer layer index of a vLLM layer name (``model.layers.7.attn``); memoised, as the names of one
+    model repeat every step."""
     match = _LAYER_RE.search(layer_name)
     return int(match.group(1)) if match else None
 

@@ -57,6 +57,9 @@ class LayerFeatures:
     sinks: Any = None
     alibi_slopes: Any = None
     attn_type: str = "DECODER"
+    # an engine feature the op does not implement (quantised output or KV
+    # cache, shared KV, soft-capped logits, cascade attention)
+    unsupported_mode: bool = False
 
 
 def _dtype_name(dtype: object) -> str:
@@ -69,7 +72,14 @@ def _contiguous(t: object) -> bool:
 
 
 def _shape(t: object) -> tuple[int, ...]:
-    return tuple(int(x) for x in getattr(t, "shape", ()))
+    shape = getattr(t, "shape", ())
+    # torch.Size is already a tuple of ints; anything else is normalised
+    return shape if type(shape).__name__ == "Size" else tuple(int(x) for x in shape)
+
+
+def leading_rows(t: Any, n: int) -> Any:
+    """The first ``n`` rows of ``t`` (``t`` itself when it has exactly ``n``: no view to build per call)."""
+    return t if t.shape[0] == n else t[:n]
 
 
 def _model_reason(features: LayerFeatures, config: PluginConfig) -> FallbackReason:
@@ -81,8 +91,8 @@ def _model_reason(features: LayerFeatures, config: PluginConfig) -> FallbackReas
         return FallbackReason.NON_CAUSAL
     if not config.kernel.has_supported_geometry:
         return FallbackReason.GEOMETRY_UNSUPPORTED
-    if (features.sliding_window is not None or features.sinks is not None
-            or features.alibi_slopes is not None or "ENCODER" in features.attn_type.upper()):
+    if (features.sliding_window is not None or features.sinks is not None or features.alibi_slopes is not None
+            or features.unsupported_mode or "ENCODER" in features.attn_type.upper()):
         return FallbackReason.MODEL_UNSUPPORTED
     return FallbackReason.NONE
 
@@ -171,7 +181,7 @@ class TriangleMixRouter:
     def _log_if_due(self) -> None:
         log_if_due(self.stats, logger)
 
-    def _fallback(self, plan: TriangleBatchPlan, layer_index: int | None, reason: FallbackReason) -> None:
+    def _count_fallback(self, plan: TriangleBatchPlan, layer_index: int | None, reason: FallbackReason) -> None:
         # Graph-capture metadata is a reusable dummy, not a scheduled request.
         if reason is not FallbackReason.GRAPH_CAPTURE:
             self.stats.record_planner_decision(plan)
@@ -182,36 +192,53 @@ class TriangleMixRouter:
 
     def prefill_attention(self, *, layer_name: str, plan: TriangleBatchPlan | None, query, key_cache, value_cache,
                           block_table, output, softmax_scale: float, features: LayerFeatures = LayerFeatures(),
-                          capturing: bool = False):
-        """Attention of one layer for the step's chunk, written into ``output``."""
+                          capturing: bool = False, fallback: Callable[[], Any] | None = None,
+                          before_direct: Callable[[], None] | None = None):
+        """Attention of one layer for the step's chunk, written into ``output``.
+
+        ``fallback`` replaces the dense companion kernel as the non-direct
+        path (an engine passes its own attention call); ``before_direct`` runs
+        once the direct path is chosen, right before the launch (an engine
+        writes the chunk's K/V into the cache there).  A failure in either
+        one, like a failing launch, is counted and falls back.
+        """
         seq_len = plan.requests[0].seq_len if plan is not None else None
         dense_kwargs = dict(query=query, key_cache=key_cache, value_cache=value_cache, block_table=block_table,
                             output=output, scale=softmax_scale)
-        if not self.config.enabled or plan is None or not self.config.kernel.uses_layer(layer_name):
+
+        def dense():
+            if fallback is not None:
+                return fallback()
             if seq_len is None:
                 raise ValueError("dense fallback needs the chunk's seq_len from a plan")
             return self._dense_fallback(seq_len=seq_len, **dense_kwargs)
+
+        if not self.config.enabled or plan is None or not self.config.kernel.uses_layer(layer_name):
+            return dense()
         layer_index = extract_layer_index(layer_name)
         reason = dispatch_reason(config=self.config, plan=plan, features=features, query=query, output=output,
                                  key_cache=key_cache, value_cache=value_cache, block_table=block_table,
                                  capturing=capturing, native_ready=self._native_ready())
         if reason is not FallbackReason.NONE:
-            self._fallback(plan, layer_index, reason)
-            return self._dense_fallback(seq_len=seq_len, **dense_kwargs)
+            self._count_fallback(plan, layer_index, reason)
+            return dense()
         request = plan.requests[0]
         rows = request.query_len
         started = time.perf_counter_ns()
         try:
-            self._direct(query=query[:rows], key_cache=key_cache, value_cache=value_cache, block_table=block_table,
-                         seq_len=request.seq_len, prompt_len=request.prompt_len, output=output[:rows],
+            if before_direct is not None:
+                before_direct()
+            self._direct(query=leading_rows(query, rows), key_cache=key_cache, value_cache=value_cache,
+                         block_table=block_table, seq_len=request.seq_len, prompt_len=request.prompt_len,
+                         output=leading_rows(output, rows),
                          softmax_scale=float(softmax_scale), config=self.config.kernel)
         except Exception:
             self.stats.record_runtime_error(stage="direct_launch")
             if self.config.strict:
                 raise
-            logger.exception("TriangleMix direct launch failed at layer %s; using the dense kernel", layer_name)
-            self._fallback(plan, layer_index, FallbackReason.DIRECT_LAUNCH_ERROR)
-            return self._dense_fallback(seq_len=seq_len, **dense_kwargs)
+            logger.exception("TriangleMix direct launch failed at layer %s; using the fallback path", layer_name)
+            self._count_fallback(plan, layer_index, FallbackReason.DIRECT_LAUNCH_ERROR)
+            return dense()
         enqueue_ns = time.perf_counter_ns() - started
         self.stats.record_planner_decision(plan)
         self.stats.record_layer_dispatch(plan_id=plan.plan_id, layer_index=layer_index, saved_qk=request.saved_qk,
