@@ -169,14 +169,17 @@ __device__ __forceinline__ void decode_item(const KernelParams& p, int sparse_be
 // 64 multiplies of the O rescale are skipped on most tiles.
 constexpr float kLazyRescale = 8.0f;
 
-// The value held by the lane 32 positions away (v_permlane32_swap: a VALU
-// exchange of the two 32-lane halves, no LDS round trip).
-__device__ __forceinline__ float other_half(float x) {
+// max / sum of x over the lane pair (i, i ^ 32), in every lane: v_permlane32_swap
+// hands each lane both halves, so no lane select is needed.
+__device__ __forceinline__ float half_max(float x) {
   const unsigned u = __float_as_uint(x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  // r[0]: lanes 0-31 keep x, lanes 32-63 get x of lanes 0-31; r[1]: lanes
-  // 0-31 get x of lanes 32-63, lanes 32-63 keep x.
-  return __uint_as_float(__lane_id() < 32 ? r[1] : r[0]);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Key offset inside the tile of accumulator element v, for lanes of the
@@ -419,11 +422,14 @@ triangle_paged_attention_kernel(KernelParams p) {
 #pragma unroll
   for (int m = 0; m < kHeadDim / 32; ++m) o_acc[m] = f32x16_t{};
 
-  // Per-lane LDS read offsets inside a tile (loop invariant).
+  // Per-lane LDS read offsets inside a slot (loop invariant): this wave's
+  // tile plus the lane's position in it, so that a read address is the slot's
+  // constant base plus one of these (no per-iteration address arithmetic).
+  const int tile_off = kq * kTileBytes;
   // K (A operand of QK): row n, chunk 2c + half.
   int k_off[kHeadDim / 16];
 #pragma unroll
-  for (int c = 0; c < kHeadDim / 16; ++c) k_off[c] = n * kRowBytes + 16 * k_slot(n, 2 * c + half);
+  for (int c = 0; c < kHeadDim / 16; ++c) k_off[c] = tile_off + n * kRowBytes + 16 * k_slot(n, 2 * c + half);
   // V (A operand of PV, transposed read): 16-lane group g = lane/16 reads key
   // quad 4*(g/2) + (lane%16)/4 at dims 32m + 16*(g%2) + 4*(lane%4); the key
   // offsets 16j and +8 are multiples of 4, so they do not change the swizzle.
@@ -432,10 +438,9 @@ triangle_paged_attention_kernel(KernelParams p) {
 #pragma unroll
   for (int m = 0; m < kHeadDim / 32; ++m) {
     const int d = 32 * m + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    v_off[m] = tr_key * kRowBytes + 16 * v_slot(tr_key, d >> 3) + 2 * (d & 7);
+    v_off[m] = tile_off + tr_key * kRowBytes + 16 * v_slot(tr_key, d >> 3) + 2 * (d & 7);
   }
   const float c2 = p.scale_log2;
-  const int tile_off = kq * kTileBytes;    // this wave's tile inside a slot
   const int dma_off = dma_u * kTileBytes;  // the tile this wave loads
 
   // Mask of tile ti of the item (in place, before its row max), applied only
@@ -466,7 +471,8 @@ triangle_paged_attention_kernel(KernelParams p) {
   // before all K/V DMA).
   bf16x8_t qreg[kHeadDim / 16];
   {
-    const unsigned qb = (unsigned)(size_t)TM_LDS(q_lds + hl * kRowBlock * kRowBytes);
+    // k_off includes the K tile offset; Q has no tiles, so take it back out.
+    const unsigned qb = (unsigned)(size_t)TM_LDS(q_lds + hl * kRowBlock * kRowBytes) - (unsigned)tile_off;
     asm volatile(
         "ds_read_b128 %0, %8\n\t"
         "ds_read_b128 %1, %9\n\t"
@@ -489,7 +495,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     // All eight K operands are read before the MFMA chain starts.
     bf16x8_t k0f[kHeadDim / 16];
 #pragma unroll
-    for (int c = 0; c < kHeadDim / 16; ++c) k0f[c] = k_operand(k_lds0 + tile_off, k_off, c);
+    for (int c = 0; c < kHeadDim / 16; ++c) k0f[c] = k_operand(k_lds0, k_off, c);
     __builtin_amdgcn_sched_barrier(0);
     s_a = f32x16_t{};
 #pragma unroll
@@ -498,7 +504,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     float tmax = -INFINITY;
 #pragma unroll
     for (int v = 0; v < 16; ++v) tmax = fmaxf(tmax, s_a[v]);
-    m_tile = fmaxf(tmax, other_half(tmax)) * c2;
+    m_tile = half_max(tmax) * c2;
   }
   // O and the row sum are still zero: the first tile's max becomes the state
   // directly (the first update then rescales nothing).
@@ -534,11 +540,9 @@ triangle_paged_attention_kernel(KernelParams p) {
     // four before the PV steps that need them, so the VALU work is spread
     // over both blocks' MFMAs.  K operands are read kReadAhead steps ahead of
     // their MFMA; the last steps also start the V reads of block 2.
-    const char* kt = kr + tile_off;
-    const char* vt = vr + tile_off;
     bf16x8_t kf[8], va[8];
 #pragma unroll
-    for (int k = 0; k < kReadAhead; ++k) kf[k] = k_operand(kt, k_off, k);
+    for (int k = 0; k < kReadAhead; ++k) kf[k] = k_operand(kr, k_off, k);
     float px[16];
     float rsum = 0.0f;
     auto expo = [&](int e) {
@@ -549,9 +553,9 @@ triangle_paged_attention_kernel(KernelParams p) {
     for (int k = 0; k < 8; ++k) {
       dma(pf_rsrc, pf_lds, k);
       if (k + kReadAhead < 8) {
-        kf[k + kReadAhead] = k_operand(kt, k_off, k + kReadAhead);
+        kf[k + kReadAhead] = k_operand(kr, k_off, k + kReadAhead);
       } else {
-        va[k + kReadAhead - 8] = v_operand(vt, v_off, k + kReadAhead - 8);
+        va[k + kReadAhead - 8] = v_operand(vr, v_off, k + kReadAhead - 8);
       }
       s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qreg[k], k == 0 ? f32x16_t{} : s_nxt, 0, 0, 0);
       expo(k);
@@ -573,7 +577,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     float tmax = -INFINITY;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      if (k + kReadAhead < 8) va[k + kReadAhead] = v_operand(vt, v_off, k + kReadAhead);
+      if (k + kReadAhead < 8) va[k + kReadAhead] = v_operand(vr, v_off, k + kReadAhead);
       if (k < 4) {
         expo(12 + k);
         if (k == 3) {
@@ -582,11 +586,11 @@ triangle_paged_attention_kernel(KernelParams p) {
         }
       }
       o_acc[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[k], pb[k >> 2], o_acc[k & 3], 0, 0, 0);
-      tmax = fmaxf(tmax, fmaxf(s_nxt[2 * k], s_nxt[2 * k + 1]));
+      tmax = fmaxf(fmaxf(tmax, s_nxt[2 * k]), s_nxt[2 * k + 1]);
       __builtin_amdgcn_sched_barrier(0);
     }
     l_run += rsum;
-    m_tile = fmaxf(tmax, other_half(tmax)) * c2;
+    m_tile = half_max(tmax) * c2;
   };
   for (int it = 0; it < num_iters; it += 2) {
     iteration(it, s_a, s_b, k_lds1, v_lds0, k_lds0, v_lds1);
@@ -676,7 +680,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   }
 
   if (nsplit == 1) {
-    const float l_tot = l_run + other_half(l_run);  // the two 32-lane halves hold one row
+    const float l_tot = half_sum(l_run);  // the two 32-lane halves hold one row
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (!row_active) return;
     __bf16* orow = p.out + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim;
@@ -794,7 +798,7 @@ triangle_paged_attention_combine_kernel(KernelParams p) {
       for (int g = 0; g < 4; ++g) ot[g] += os[b][g] * wb;
     }
   }
-  const float l_tot = lt + other_half(lt);  // the two 32-lane halves hold one row
+  const float l_tot = half_sum(lt);  // the two 32-lane halves hold one row
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (!row_active) return;
   __bf16* orow = p.out + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim;
