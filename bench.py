@@ -28,6 +28,10 @@ Reported JSON line (rank 0 only):
 
 Other workloads (not the headline line; one JSON line each):
 
+* ``--workload config1`` -- the reference's CPU-runnable case: one launch,
+  rows 2357..2868 of a 2869-token prompt (384 sparse rows and the 128-row
+  dense tail);
+
 * ``--workload config3`` -- L=8320 in chunks of 2048 with 1 % of the K
   entries set to +-8 (the same legs as above);
 * ``--workload config4`` -- long-context curve, chunk 2048: the whole prefill
@@ -71,7 +75,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--only", choices=("sparse", "dense"), help="run one kernel only (for profiling)")
-    ap.add_argument("--workload", choices=("config2", "config3", "config4", "config5"), default="config2")
+    ap.add_argument("--workload", choices=("config1", "config2", "config3", "config4", "config5"),
+                    default="config2")
     ap.add_argument("--outliers", type=float, default=None, help="fraction of K entries set to +-8")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run 5 plain device copies of MIB MiB (scales rocprofv3 FETCH/WRITE_SIZE)")
@@ -88,8 +93,8 @@ def main() -> int:
     import torch
 
     from trianglemix import native
-    from trianglemix.workload import (SCALE, chunk_bytes, chunk_flops, executed_flops, kv_bytes, make_cache,
-                                      make_query, prompt_chunks)
+    from trianglemix.workload import (SCALE, Chunk, chunk_bytes, chunk_flops, executed_flops, kv_bytes,
+                                      make_cache, make_query, prompt_chunks)
 
     if args.workload == "config4":
         return config4_curve(args)
@@ -103,7 +108,11 @@ def main() -> int:
     native.load_hip_library()
     native.load_triangle_mix_adapter()
     dev = torch.device("cuda:0")
-    chunks = prompt_chunks(args.prompt, args.chunk)
+    if args.workload == "config1":
+        args.prompt, args.chunk = 2869, 512
+        chunks = [Chunk(2357, 2869, 2869)]
+    else:
+        chunks = prompt_chunks(args.prompt, args.chunk)
 
     k, v, bt = make_cache(args.prompt, args.seed, std=1.0, outlier_frac=args.outliers or 0.0)
     qfull = make_query(args.prompt, args.seed + 1, std=1.0)
@@ -224,6 +233,9 @@ def main() -> int:
 
     workload = (f"config2: one request, L={args.prompt}, chunked prefill {args.chunk} x {n} chunks, "
                 "Hq=32 Hkv=8 D=128 page=128, one layer")
+    if args.workload == "config1":
+        workload = ("config1: one launch, rows 2357..2868 of a 2869-token prompt (384 sparse rows + 128-row "
+                    "dense tail), Hq=32 Hkv=8 D=128 page=128, one layer")
     if args.workload == "config3":
         workload = (f"config3: one request, L={args.prompt}, chunked prefill {args.chunk} x {n} chunks, "
                     f"{args.outliers:.0%} of K entries +-8, Hq=32 Hkv=8 D=128 page=128, one layer")
