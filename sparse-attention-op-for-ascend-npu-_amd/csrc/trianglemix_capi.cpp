@@ -56,44 +56,63 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
   return TM_OK;
 }
 
-// Split-KV sizing.  A chunk runs as 16 workgroups (8 KV heads x 2 head
-// pairs) per work item, one workgroup per CU, so each (KV head, head pair)
-// has kSlots of the 256 CUs.  A row block of n tiles is cut into
+// Workgroup shape.  Chunks of at least kHalvesMinRowBlocks row blocks run
+// with KV halves (the four heads of a GQA group per workgroup, 8 workgroups
+// per work item): their 8 x row blocks workgroups still cover the 256 CUs,
+// each K/V tile then serves four heads, and a sparse row block's 18 tiles
+// split evenly.  Smaller chunks run with KV quarters (two heads per
+// workgroup, 16 workgroups per item) to fill the CUs.
+constexpr int kHalvesMinRowBlocks = 32;
+
+int kv_parts_for(int num_row_blocks) { return num_row_blocks >= kHalvesMinRowBlocks ? 2 : 4; }
+
+// Split-KV sizing.  A work item runs as 16 (KV quarters) or 8 (KV halves)
+// workgroups, one per CU, so each of the item's workgroup positions has
+// slots = 256 / that many CUs.  A row block of n tiles is cut into
 // ceil(n / T) near-equal items of at most T tiles; T is chosen by simulating
-// the greedy dispatch of the items (issued heaviest row block first) onto
-// kSlots slots, an item costing kItemFixedTiles + its tiles, and taking the T
-// with the shortest makespan (ties: larger T, fewer partials); a plan that
-// splits anything also pays for the combine kernel.  T is at least
-// kMinSplitTiles (1024 keys: a split's fp32 partial of 66 KB stays small next
-// to the K/V it reads, 16 KB per 32-key tile) and at most kMaxItemTiles.
-constexpr int kSlots = 16;
-constexpr int kItemFixedTiles = 15;  // start-up, merge and store of an item, in tile times (measured)
-constexpr int kCombineTiles = 15;    // the combine kernel a plan with splits adds, in tile times (measured)
+// the greedy dispatch of the items (issued heaviest row block first) onto the
+// slots, an item costing a fixed start-up + merge + store cost plus its tiles,
+// and taking the T with the shortest makespan (ties: larger T, fewer
+// partials); a plan that splits anything also pays for the combine kernel.
+// Costs are in tile times: a KV-halves workgroup runs a tile per part and
+// iteration as a quarters one does, but over two parts, so its fixed costs
+// weigh half as many tile times.  T is at least kMinSplitTiles (1024 keys: a
+// split's fp32 partial of 66 KB stays small next to the K/V it reads, 16 KB
+// per 32-key tile) and at most kMaxItemTiles.
+struct PlanCosts {
+  int slots;
+  int item_fixed_tiles;  // start-up, merge and store of an item (measured)
+  int combine_tiles;     // the combine kernel a plan with splits adds (measured)
+};
+constexpr PlanCosts kQuarterCosts{16, 15, 15};
+constexpr PlanCosts kHalfCosts{32, 8, 8};
+constexpr int kMaxSlots = 32;
+PlanCosts plan_costs(int kv_parts) { return kv_parts == 2 ? kHalfCosts : kQuarterCosts; }
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 // Beyond this many items per candidate the simulation is skipped (its host
-// cost would show): T then spreads the chunk's tiles over kSlots items.
+// cost would show): T then spreads the chunk's tiles over one item per slot.
 constexpr int64_t kMaxSimulatedItems = 4096;
 constexpr int kSplitStep = 4;  // candidate T: kMaxItemTiles, kMaxItemTiles - 4, ..., >= kMinSplitTiles
 
-int64_t simulated_makespan(const std::vector<int>& row_tiles, int T) {
-  int64_t slot[kSlots] = {};
+int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanCosts& c) {
+  int64_t slot[kMaxSlots] = {};
   for (const int n : row_tiles) {
     const int pieces = (n + T - 1) / T;
     for (int i = 0; i < pieces; ++i) {
       const int size = (int)((int64_t)(i + 1) * n / pieces - (int64_t)i * n / pieces);
       int best = 0;
-      for (int k = 1; k < kSlots; ++k) best = slot[k] < slot[best] ? k : best;
-      slot[best] += kItemFixedTiles + size;
+      for (int k = 1; k < c.slots; ++k) best = slot[k] < slot[best] ? k : best;
+      slot[best] += c.item_fixed_tiles + size;
     }
   }
   int64_t makespan = 0;
   bool any_split = false;
-  for (const int64_t f : slot) makespan = f > makespan ? f : makespan;
+  for (int k = 0; k < c.slots; ++k) makespan = slot[k] > makespan ? slot[k] : makespan;
   for (const int n : row_tiles) any_split = any_split || n > T;
-  return makespan + (any_split ? kCombineTiles : 0);
+  return makespan + (any_split ? c.combine_tiles : 0);
 }
 
-int choose_tiles_per_split(const std::vector<int>& row_tiles) {
+int choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c) {
   int64_t total = 0;
   int longest = 0;
   for (const int n : row_tiles) {
@@ -102,13 +121,13 @@ int choose_tiles_per_split(const std::vector<int>& row_tiles) {
   }
   if (longest <= kMinSplitTiles) return kMinSplitTiles;  // nothing to split
   if (total / kMinSplitTiles > kMaxSimulatedItems) {
-    const int64_t per_item = (total + kSlots - 1) / kSlots;
+    const int64_t per_item = (total + c.slots - 1) / c.slots;
     return (int)(per_item < kMinSplitTiles ? kMinSplitTiles : (per_item > tmx::kMaxItemTiles ? tmx::kMaxItemTiles : per_item));
   }
   int best_t = tmx::kMaxItemTiles;
-  int64_t best = simulated_makespan(row_tiles, best_t);
+  int64_t best = simulated_makespan(row_tiles, best_t, c);
   for (int t = tmx::kMaxItemTiles - kSplitStep; t >= kMinSplitTiles; t -= kSplitStep) {
-    const int64_t ms = simulated_makespan(row_tiles, t);
+    const int64_t ms = simulated_makespan(row_tiles, t, c);
     if (ms < best) {
       best = ms;
       best_t = t;
@@ -140,7 +159,7 @@ int cached_tiles_per_split(const PlanKey& key) {
     row_tiles[(size_t)o] = tmx::row_block_splits((int)o, (int)key.num_row_blocks, (int)key.query_start,
                                                  (int)key.seq_len, (int)key.sparse_begin, (int)key.sparse_end, 1);
   }
-  const int t = choose_tiles_per_split(row_tiles);
+  const int t = choose_tiles_per_split(row_tiles, plan_costs(kv_parts_for((int)key.num_row_blocks)));
   keys[next] = key;
   values[next] = t;
   next = (next + 1) % kEntries;
@@ -153,7 +172,7 @@ int cached_tiles_per_split(const PlanKey& key) {
 constexpr int64_t kMaxItemsPerHead = int64_t(1) << 26;
 
 struct Geometry {
-  int sparse_begin, sparse_end, num_row_blocks, tiles_per_split;
+  int sparse_begin, sparse_end, num_row_blocks, tiles_per_split, kv_parts;
   int64_t items_per_head;
   bool any_split;
   int64_t workspace_bytes;
@@ -164,6 +183,7 @@ Geometry make_geometry(bool sparse, int64_t query_tokens, int64_t query_start, i
   g.sparse_begin = sparse ? tmx::kSparseBegin : 0;
   g.sparse_end = sparse ? (int)(prompt_len > tmx::kDenseTail ? prompt_len - tmx::kDenseTail : 0) : 0;
   g.num_row_blocks = (int)((query_tokens + tmx::kRowBlock - 1) / tmx::kRowBlock);
+  g.kv_parts = kv_parts_for(g.num_row_blocks);
   g.tiles_per_split = cached_tiles_per_split(
       PlanKey{g.num_row_blocks, query_start, seq_len, g.sparse_begin, g.sparse_end});
   bool any_split = false;
@@ -252,7 +272,7 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   p.any_split = g.any_split ? 1 : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
   const hipError_t err =
-      tmx::launch_triangle_paged_attention(p, sparse, g.any_split, static_cast<hipStream_t>(stream));
+      tmx::launch_triangle_paged_attention(p, sparse, g.any_split, g.kv_parts, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     return fail(TM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   }

@@ -97,8 +97,11 @@ struct KernelParams {
 
 // Enqueues the attention kernel (TriangleMix mask when `sparse`, plain causal
 // otherwise) and, when some row block is split, the combine kernel that
-// merges its partials (same stream, in order).
-hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, bool any_split, hipStream_t stream);
+// merges its partials (same stream, in order).  kv_parts picks the workgroup
+// shape: 4 (two query heads x KV quarters, items_per_head x 16 workgroups) or
+// 2 (the four heads of the GQA group x KV halves, items_per_head x 8).
+hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, bool any_split, int kv_parts,
+                                           hipStream_t stream);
 
 // Enqueues the paged KV write: token i's K and V rows ([8, 128] bf16, row
 // strides key_stride / value_stride in elements, multiples of 8) go to cache

@@ -100,15 +100,28 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 #define TM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-constexpr int kHeadsPerGroup = 2;                // query heads per workgroup
-constexpr int kQuarters = 4;                     // KV quarters per workgroup
-constexpr int kWaves = kHeadsPerGroup * kQuarters;
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kGroupsPerKvHead = kGroup / kHeadsPerGroup;
 constexpr int kRowBytes = kHeadDim * 2;          // 256 B: one key row
 constexpr int kTileBytes = kKvTile * kRowBytes;  // 8 KB: K or V of one tile
-constexpr int kSlotBytes = kQuarters * kTileBytes;  // the tiles of all quarters of one iteration
 constexpr int kDmaPerTile = kTileBytes / 1024;   // 1 KB (4 key rows) per DMA instruction
+
+// Workgroup shape: the eight waves are kParts KV parts x kHeads query heads.
+// P = 4 (two heads, KV quarters) puts a 512-token chunk's 16 row blocks on
+// 256 workgroups; P = 2 (all four heads of the GQA group, KV halves) loads
+// each K/V tile once for four heads and cuts an aligned sparse row block's 18
+// tiles into 9 + 9, for chunks with enough row blocks to fill the CUs.
+template <int P>
+struct Shape {
+  static constexpr int kParts = P;                      // KV parts: tiles kq, kq + P, ...
+  static constexpr int kHeads = kWaves / P;             // query heads per workgroup
+  static constexpr int kWgPerKvHead = kGroup / kHeads;  // workgroups per (row block, KV head)
+  static constexpr int kSlotBytes = P * kTileBytes;     // the tiles of all parts of one iteration
+  static constexpr int kDmaPerWave = 2 * P;             // DMA instructions per wave and iteration
+  static constexpr int kWavesPerTile = kDmaPerTile / kDmaPerWave;  // waves sharing one tile's DMA
+  static constexpr int kOwned = (kHeadDim / 32) / P;    // 32-wide d-blocks a wave keeps in the merge
+  static_assert((P == 4 || P == 2) && kHeads * P == kWaves, "supported shapes: 4 x 2 and 2 x 4");
+};
 // Buffer-resource word 3 for raw (unformatted, stride 0) dword loads on gfx9.
 constexpr int kBufferFlags = 0x00020000;
 // A buffer offset past every range used here: such a load returns 0.
@@ -116,16 +129,19 @@ constexpr unsigned kOutOfRange = 0x40000000u;
 
 static_assert(kKvTile == 32 && kPageSize % kKvTile == 0, "a tile must stay inside one page");
 static_assert(kRowBlock == 32, "one MFMA column per query token");
-static_assert(kWaves == 2 * kQuarters && kDmaPerTile == 8,
-              "each wave loads one tile per iteration, one DMA instruction per MFMA step");
+static_assert(kDmaPerTile == 8, "a tile is eight 1 KB DMA instructions, one per MFMA step at most");
 
 // Wait until every LDS DMA (and other vector-memory load) this wave issued has
 // landed: s_waitcnt vmcnt(0), expcnt / lgkmcnt unconstrained.  Each wave runs
 // it before a barrier that publishes DMA'd tiles to the other waves -- the
 // barrier alone does not order the DMA's LDS writes.
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-// All but the last eight vector-memory operations of this wave have landed.
-__device__ __forceinline__ void wait_dma_but8() { __builtin_amdgcn_s_waitcnt(0x0F78); }
+// All but the last N (< 16) vector-memory operations of this wave have landed.
+template <int N>
+__device__ __forceinline__ void wait_dma_but() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
 
 __device__ __forceinline__ int k_slot(int row, int chunk) { return chunk ^ (row & 15); }
 __device__ __forceinline__ int v_slot(int row, int chunk) { return chunk ^ ((row & 3) << 2); }
@@ -243,21 +259,23 @@ __device__ __forceinline__ float softmax_update(float m_tile, float& m_run, floa
   return m_run == -INFINITY ? 0.0f : m_run;
 }
 
-template <bool kSparse>
+template <bool kSparse, int P>
 __global__ void __launch_bounds__(kThreads)
 triangle_paged_attention_kernel(KernelParams p) {
-  // K slots 0/1 and V slots 0/1: the four tiles of iteration i live in slot i % 2.
-  __shared__ __attribute__((aligned(1024))) char k_lds0[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) char k_lds1[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) char v_lds0[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) char v_lds1[kSlotBytes];
-  // Q of the workgroup's two heads: [head][row][16-byte slot], K's swizzle.
-  __shared__ __attribute__((aligned(1024))) char q_lds[kHeadsPerGroup * kRowBlock * kRowBytes];
+  using S = Shape<P>;
+  constexpr int H = S::kHeads;
+  // K slots 0/1 and V slots 0/1: the P tiles of iteration i live in slot i % 2.
+  __shared__ __attribute__((aligned(1024))) char k_lds0[S::kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) char k_lds1[S::kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) char v_lds0[S::kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) char v_lds1[S::kSlotBytes];
+  // Q of the workgroup's heads: [head][row][16-byte slot], K's swizzle.
+  __shared__ __attribute__((aligned(1024))) char q_lds[H * kRowBlock * kRowBytes];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, kept scalar
-  const int hl = wave & 1;   // query head inside the workgroup's pair
-  const int kq = wave >> 1;  // KV quarter: tiles kq, kq+4, ... of the item
+  const int hl = wave % H;   // query head inside the workgroup's heads
+  const int kq = wave / H;   // KV part: tiles kq, kq+P, ... of the item
   const int lane = tid & 63;
   const int n = lane & 31;  // MFMA column = query token of this lane
   const int half = lane >> 5;
@@ -266,8 +284,8 @@ triangle_paged_attention_kernel(KernelParams p) {
   const int sparse_end = kSparse ? p.sparse_end : 0;
 
   const int kvh = blockIdx.x % kKvHeads;
-  const int hp = (blockIdx.x / kKvHeads) % kGroupsPerKvHead;
-  const int item = blockIdx.x / (kKvHeads * kGroupsPerKvHead);
+  const int hp = (blockIdx.x / kKvHeads) % S::kWgPerKvHead;
+  const int item = blockIdx.x / (kKvHeads * S::kWgPerKvHead);
   int order, split, nsplit;
   if (p.any_split) {
     decode_item(p, sparse_begin, sparse_end, item, lane, order, split, nsplit);
@@ -284,7 +302,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   const int rb = p.num_row_blocks - 1 - order;
   const int tb = p.query_start + rb * kRowBlock;
   const int te = min(tb + kRowBlock, p.seq_len);
-  const int hq = kHeadsPerGroup * hp + hl;  // query head inside the GQA group
+  const int hq = H * hp + hl;  // query head inside the GQA group
   const int head = kvh * kGroup + hq;
   const int q = tb + n;
   const bool row_active = q < te;
@@ -301,19 +319,22 @@ triangle_paged_attention_kernel(KernelParams p) {
     t_lo = split * base + min(split, rem);
     num_tiles = base + (split < rem ? 1 : 0);
   }
-  const int num_iters = (num_tiles + kQuarters - 1) / kQuarters;
+  const int num_iters = (num_tiles + P - 1) / P;
 
-  // ---- DMA: per iteration, wave w loads one whole tile ----
-  // Waves 0-3 load the K tile of quarter w, waves 4-7 the V tile of quarter
-  // w - 4: eight wave-instructions of 1 KB (4 key rows).  Lane i of
-  // instruction j writes LDS slot (row 4j + i/16, slot i%16), so it loads the
-  // global chunk the swizzle puts in that slot.
-  const int dma_t = wave >> 2;  // 0 = K, 1 = V
-  const int dma_u = wave & 3;   // quarter
-  unsigned dma_voff[kDmaPerTile];
+  // ---- DMA: per iteration the 2P tiles (K and V of every part) ----
+  // A tile is eight wave-instructions of 1 KB (4 key rows).  With P = 4 wave w
+  // loads one whole tile (waves 0-3 the K tile of quarter w, waves 4-7 the V
+  // tile of quarter w - 4); with P = 2 two waves share a tile, four
+  // instructions each.  Lane i of instruction j writes LDS slot (row 4j + i/16,
+  // slot i%16), so it loads the global chunk the swizzle puts in that slot.
+  const int dma_tile = wave / S::kWavesPerTile;
+  const int dma_t = dma_tile / P;  // 0 = K, 1 = V
+  const int dma_u = dma_tile % P;  // part
+  const int dma_j0 = (wave % S::kWavesPerTile) * S::kDmaPerWave;  // this wave's first instruction of the tile
+  unsigned dma_voff[kDmaPerTile];  // the first kDmaPerWave are used (fixed size: see kept below)
 #pragma unroll
-  for (int j = 0; j < kDmaPerTile; ++j) {
-    const int row = 4 * j + (lane >> 4);
+  for (int j = 0; j < S::kDmaPerWave; ++j) {
+    const int row = 4 * (dma_j0 + j) + (lane >> 4);
     const int slot = dma_t == 0 ? k_slot(row, lane & 15) : v_slot(row, lane & 15);
     dma_voff[j] = (unsigned)(row * kKvHeads * kRowBytes + 16 * slot);
   }
@@ -341,20 +362,20 @@ triangle_paged_attention_kernel(KernelParams p) {
   };
   const int phys_lo = lane_page(lane);
   const int phys_hi = lane_page(64 + lane);
-  // ---- Q: the workgroup's two heads x 32 rows (16 KB), DMA'd once into LDS ----
-  // (each of the four quarter waves of a head needs all of it; loading it per
-  // wave would quadruple the start-up traffic through the CU).  Wave w loads
-  // 1 KB blocks g = 2w, 2w + 1: head g / 8, rows 4 (g % 8) .. + 3; lane i
-  // writes slot i % 16 of row 4 (g % 8) + i / 16, i.e. global chunk
+  // ---- Q: the workgroup's H heads x 32 rows (8 KB per head), DMA'd once into LDS ----
+  // (each of the P part waves of a head needs all of it; loading it per wave
+  // would multiply the start-up traffic through the CU).  Wave w loads the H
+  // 1 KB blocks g = H w .. H w + H - 1: head g / 8, rows 4 (g % 8) .. + 3;
+  // lane i writes slot i % 16 of row 4 (g % 8) + i / 16, i.e. global chunk
   // k_slot(row, i % 16).  The range ends at the block's last row: rows past
   // seq_len read 0.  Issued before the wait on the block table (no dependency).
   {
     const __amdgpu_buffer_rsrc_t q_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.query + ((size_t)(tb - p.query_start) * kQueryHeads + kvh * kGroup + kHeadsPerGroup * hp) * kHeadDim),
-        (short)0, (te - tb - 1) * kQueryHeads * kRowBytes + kHeadsPerGroup * kRowBytes, kBufferFlags);
+        (void*)(p.query + ((size_t)(tb - p.query_start) * kQueryHeads + kvh * kGroup + H * hp) * kHeadDim),
+        (short)0, (te - tb - 1) * kQueryHeads * kRowBytes + H * kRowBytes, kBufferFlags);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int g = 2 * wave + j;
+    for (int j = 0; j < H; ++j) {
+      const int g = H * wave + j;
       const int row = 4 * (g & 7) + (lane >> 4);
       const unsigned off = (unsigned)(row * kQueryHeads * kRowBytes + (g >> 3) * kRowBytes + 16 * k_slot(row, lane & 15));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rsrc, TM_LDS(q_lds + g * 1024), 16, off, 0, 0, 0);
@@ -383,21 +404,22 @@ triangle_paged_attention_kernel(KernelParams p) {
     const char* cache = reinterpret_cast<const char*>(t == 0 ? p.key_cache : p.value_cache);
     return __builtin_amdgcn_make_buffer_rsrc((void*)(cache + (size_t)row * kRowBytes), (short)0, bytes, kBufferFlags);
   };
-  // DMA instruction j of this wave's tile of one iteration.
+  // DMA instruction j of this wave's share of a tile.
   auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, char* lds_tile, int j) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TM_LDS(lds_tile + j * 1024), 16, dma_voff[j], 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, TM_LDS(lds_tile + (dma_j0 + j) * 1024), 16, dma_voff[j], 0, 0,
+                                             0);
   };
   auto issue_tile = [&](int ti, int t, char* lds_tile) {
     const __amdgpu_buffer_rsrc_t rsrc = tile_rsrc(ti, t);
 #pragma unroll
-    for (int j = 0; j < kDmaPerTile; ++j) dma(rsrc, lds_tile, j);
+    for (int j = 0; j < S::kDmaPerWave; ++j) dma(rsrc, lds_tile, j);
   };
 
   // Prologue DMA: K and V of iteration 0, K of iteration 1.
   if (dma_t == 0) {
     issue_tile(dma_u, 0, k_lds0 + dma_u * kTileBytes);
     __builtin_amdgcn_sched_barrier(0);  // K of iteration 1 goes last: the prologue wait leaves it in flight
-    issue_tile(kQuarters + dma_u, 0, k_lds1 + dma_u * kTileBytes);
+    issue_tile(P + dma_u, 0, k_lds1 + dma_u * kTileBytes);
   } else {
     issue_tile(dma_u, 1, v_lds0 + dma_u * kTileBytes);
   }
@@ -459,7 +481,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   // Only DMA data is published here, so a bare barrier (no fence: the fence
   // of __syncthreads would wait for every outstanding load) suffices.
   if (dma_t == 0) {
-    wait_dma_but8();
+    wait_dma_but<S::kDmaPerWave>();
   } else {
     wait_dma();
   }
@@ -519,7 +541,7 @@ triangle_paged_attention_kernel(KernelParams p) {
                        char* vw) {
     wait_dma();
     __syncthreads();  // DMA issued one iteration ago landed; slots kw / vw are no longer read
-    const int ti = kQuarters * it + kq;
+    const int ti = P * it + kq;
     // Ragged last iteration: the quarters without a tile idle; nothing is
     // left to prefetch in the last iteration.
     if (ti >= num_tiles) return;
@@ -529,7 +551,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     // below free of branches.
     const int pf_it = dma_t == 0 ? it + 2 : it + 1;
     const __amdgpu_buffer_rsrc_t pf_rsrc =
-        tile_rsrc(pf_it < num_iters ? kQuarters * pf_it + dma_u : num_tiles, dma_t);
+        tile_rsrc(pf_it < num_iters ? P * pf_it + dma_u : num_tiles, dma_t);
     char* pf_lds = (dma_t == 0 ? kw : vw) + dma_off;
     const float shift = softmax_update(m_tile, m_run, l_run, o_acc);
     // Block 1: the QK^T MFMAs of the next tile (run unconditionally: past the
@@ -551,7 +573,8 @@ triangle_paged_attention_kernel(KernelParams p) {
     };
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      dma(pf_rsrc, pf_lds, k);
+      // one DMA instruction every 8 / kDmaPerWave steps
+      if (k % (8 / S::kDmaPerWave) == 0) dma(pf_rsrc, pf_lds, k / (8 / S::kDmaPerWave));
       if (k + kReadAhead < 8) {
         kf[k + kReadAhead] = k_operand(kr, k_off, k + kReadAhead);
       } else {
@@ -573,7 +596,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     // exponentials (steps 0-3, before pb[1] is first used at step 4) and the
     // row max of the next tile (masked first; its state update opens the next
     // iteration).
-    mask_tile(s_nxt, ti + kQuarters);
+    mask_tile(s_nxt, ti + P);
     float tmax = -INFINITY;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -597,69 +620,78 @@ triangle_paged_attention_kernel(KernelParams p) {
     if (it + 1 < num_iters) iteration(it + 1, s_b, s_a, k_lds0, v_lds1, k_lds1, v_lds0);
   }
 
-  // ---- merge the four KV quarters through LDS ----
-  // Quarter kq keeps d-block kq and hands its three other d-blocks to their
-  // owners.  Given block index gi (0..2 among the blocks a quarter gives away)
-  // selects the slot: xo_gi[hl][quarter][v/4][lane][4] lives in k_lds0,
-  // k_lds1, v_lds0 for gi = 0, 1, 2 (16-byte accesses, one 1 KB stretch per
-  // instruction); xm / xl [hl][quarter][lane] live in v_lds1.  kq is
-  // wave-uniform, so one scalar switch picks a variant with every block and
-  // slot index fixed at compile time; both barriers stay outside the
-  // switches.
+  // ---- merge the P KV parts through LDS ----
+  // Part kq keeps the O = 4 / P d-blocks kq * O .. kq * O + O - 1 and hands
+  // its other 4 - O d-blocks to their owners.  The given-block index gi (0 ..
+  // 3 - O among the blocks a part gives away) and the giving wave w = hl * P +
+  // part select a 4 KB stretch xo(gi, w) = [v/4][lane][4] (16-byte accesses,
+  // one 1 KB stretch per instruction): for P = 4 the stretches of gi = 0, 1, 2
+  // fill k_lds0, k_lds1, v_lds0 and xm / xl [hl][part][lane] live in v_lds1;
+  // for P = 2 gi = 0 fills q_lds, gi = 1 fills k_lds0 (waves 0-3) and k_lds1
+  // (waves 4-7), and xm / xl live in v_lds0.  kq is wave-uniform, so the
+  // per-block branches are scalar; both barriers stay outside them.
   wait_dma();
   __syncthreads();  // all compute and every (empty) prefetch done; the slots are free
-  static_assert(kHeadsPerGroup * kQuarters * 16 * 64 * 4 == kSlotBytes, "one given block fills one slot");
-  auto xo = [&](int gi) {
-    return reinterpret_cast<f32x4_t*>(gi == 0 ? k_lds0 : (gi == 1 ? k_lds1 : v_lds0));
-  };
-  float* xm = reinterpret_cast<float*>(v_lds1);
-  float* xl = xm + kHeadsPerGroup * kQuarters * 64;
-  const int self = hl * kQuarters + kq;
-  auto give = [&](auto kq_c) {
-    constexpr int KQ = decltype(kq_c)::value;
-#pragma unroll
-    for (int m = 0; m < kHeadDim / 32; ++m) {
-      if (m == KQ) continue;
-      const int gi = m < KQ ? m : m - 1;  // index of block m among those this quarter gives away
-      f32x4_t* dst = xo(gi) + self * 4 * 64 + lane;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        dst[g * 64] = f32x4_t{o_acc[m][4 * g], o_acc[m][4 * g + 1], o_acc[m][4 * g + 2], o_acc[m][4 * g + 3]};
-      }
+  constexpr int O = S::kOwned;
+  static_assert(P != 4 || H * P * 4 * 64 * 16 == S::kSlotBytes, "P = 4: one given block of all waves fills a slot");
+  static_assert(P != 2 || (H * P * 4 * 64 * 16 == H * kRowBlock * kRowBytes && 4 * 4 * 64 * 16 == S::kSlotBytes),
+                "P = 2: one given block of all waves fills q_lds, half of one fills a slot");
+  auto xo = [&](int gi, int w) -> f32x4_t* {
+    if constexpr (P == 4) {
+      return reinterpret_cast<f32x4_t*>(gi == 0 ? k_lds0 : (gi == 1 ? k_lds1 : v_lds0)) + w * 4 * 64;
+    } else {
+      if (gi == 0) return reinterpret_cast<f32x4_t*>(q_lds) + w * 4 * 64;
+      return reinterpret_cast<f32x4_t*>(w < 4 ? k_lds0 : k_lds1) + (w & 3) * 4 * 64;
     }
   };
-  switch (kq) {
-    case 0: give(std::integral_constant<int, 0>{}); break;
-    case 1: give(std::integral_constant<int, 1>{}); break;
-    case 2: give(std::integral_constant<int, 2>{}); break;
-    default: give(std::integral_constant<int, 3>{}); break;
+  float* xm = reinterpret_cast<float*>(P == 4 ? v_lds1 : v_lds0);
+  float* xl = xm + H * P * 64;
+  const int self = hl * P + kq;
+  // Index of d-block m among the blocks part r gives away (m is not r's).
+  auto given_index = [](int m, int r) { return m < r * O ? m : m - O; };
+  // Every o_acc / kept index below is a compile-time constant and each d-block
+  // takes its own uniform branch: arms that differ only in which accumulator
+  // they touch would be merged by the compiler into one arm addressing o_acc
+  // through a pointer, which forces o_acc out of registers for the whole loop.
+#pragma unroll
+  for (int m = 0; m < kHeadDim / 32; ++m) {
+    if (m / O == kq) continue;
+    f32x4_t* dst = xo(given_index(m, kq), self) + lane;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      dst[g * 64] = f32x4_t{o_acc[m][4 * g], o_acc[m][4 * g + 1], o_acc[m][4 * g + 2], o_acc[m][4 * g + 3]};
+    }
   }
   xm[self * 64 + lane] = m_run;
   xl[self * 64 + lane] = l_run;
   __syncthreads();
-  f32x16_t kept;
+  // The merged (unnormalised) d-blocks kq * O + o.  Local arrays keep a fixed
+  // size (the largest shape's): hipcc's host pass drops a kernel template
+  // whose local arrays have a size that depends on the template parameters.
+  f32x16_t kept[kHeadDim / 32 / 2];
   {
-    float mq[kQuarters], lq[kQuarters];
+    float mq[4], lq[4];  // the first P are used
     float mt = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < kQuarters; ++r) {
-      mq[r] = xm[(hl * kQuarters + r) * 64 + lane];
-      lq[r] = xl[(hl * kQuarters + r) * 64 + lane];
+    for (int r = 0; r < P; ++r) {
+      mq[r] = xm[(hl * P + r) * 64 + lane];
+      lq[r] = xl[(hl * P + r) * 64 + lane];
       mt = fmaxf(mt, mq[r]);
     }
     const float mu = mt == -INFINITY ? 0.0f : mt;
     float lt = 0.0f;
 #pragma unroll
-    for (int r = 0; r < kQuarters; ++r) lt += lq[r] * __builtin_amdgcn_exp2f(mq[r] - mu);
-    auto gather = [&](auto kq_c) {
-      constexpr int KQ = decltype(kq_c)::value;
-      f32x16_t acc = o_acc[KQ] * __builtin_amdgcn_exp2f(m_run - mu);
+    for (int r = 0; r < P; ++r) lt += lq[r] * __builtin_amdgcn_exp2f(mq[r] - mu);
+    const float self_scale = __builtin_amdgcn_exp2f(m_run - mu);
 #pragma unroll
-      for (int r = 0; r < kQuarters; ++r) {
-        if (r == KQ) continue;
+    for (int m = 0; m < kHeadDim / 32; ++m) {
+      if (m / O != kq) continue;
+      f32x16_t acc = o_acc[m] * self_scale;
+#pragma unroll
+      for (int r = 0; r < P; ++r) {
+        if (r == kq) continue;
         const float a = __builtin_amdgcn_exp2f(mq[r] - mu);
-        const int gi = KQ < r ? KQ : KQ - 1;  // index of block KQ among those quarter r gives away
-        const f32x4_t* src = xo(gi) + (hl * kQuarters + r) * 4 * 64 + lane;
+        const f32x4_t* src = xo(given_index(m, r), hl * P + r) + lane;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4_t x = src[g * 64];
@@ -667,13 +699,7 @@ triangle_paged_attention_kernel(KernelParams p) {
           for (int e = 0; e < 4; ++e) acc[4 * g + e] += x[e] * a;
         }
       }
-      return acc;
-    };
-    switch (kq) {
-      case 0: kept = gather(std::integral_constant<int, 0>{}); break;
-      case 1: kept = gather(std::integral_constant<int, 1>{}); break;
-      case 2: kept = gather(std::integral_constant<int, 2>{}); break;
-      default: kept = gather(std::integral_constant<int, 3>{}); break;
+      kept[m % O] = acc;
     }
     l_run = lt;
     m_run = mt;
@@ -685,11 +711,14 @@ triangle_paged_attention_kernel(KernelParams p) {
     if (!row_active) return;
     __bf16* orow = p.out + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      bf16x4_t o4;
+    for (int o = 0; o < O; ++o) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(kept[4 * g + e] * inv);
-      *reinterpret_cast<bf16x4_t*>(orow + 32 * kq + 8 * g + 4 * half) = o4;
+      for (int g = 0; g < 4; ++g) {
+        bf16x4_t o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(kept[o][4 * g + e] * inv);
+        *reinterpret_cast<bf16x4_t*>(orow + 32 * (kq * O + o) + 8 * g + 4 * half) = o4;
+      }
     }
     return;
   }
@@ -697,15 +726,18 @@ triangle_paged_attention_kernel(KernelParams p) {
   // ---- split-KV: publish this split's partial; the combine kernel merges ----
   // Layout per (KV head, item): O [hq][m][v/4][lane][v%4], then row max
   // [hq][lane], then the lane's partial row sum [hq][lane] -- every access is
-  // a lane-contiguous 16- or 4-byte vector.  The two head-pair workgroups
-  // write disjoint heads, the four quarters disjoint d-blocks.
+  // a lane-contiguous 16- or 4-byte vector.  Workgroups of one item write
+  // disjoint heads, the parts disjoint d-blocks.
   float* part = p.partials + ((size_t)kvh * p.items_per_head + item) * kPartialFloats;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const f32x4_t o4 = {kept[4 * g], kept[4 * g + 1], kept[4 * g + 2], kept[4 * g + 3]};
-    *reinterpret_cast<f32x4_t*>(part + (((hq * 4 + kq) * 4 + g) * 64 + lane) * 4) = o4;
+  for (int o = 0; o < O; ++o) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4_t o4 = {kept[o][4 * g], kept[o][4 * g + 1], kept[o][4 * g + 2], kept[o][4 * g + 3]};
+      *reinterpret_cast<f32x4_t*>(part + (((hq * 4 + kq * O + o) * 4 + g) * 64 + lane) * 4) = o4;
+    }
   }
-  if (kq == 0) {  // every quarter holds the same merged row max and row sum
+  if (kq == 0) {  // every part holds the same merged row max and row sum
     part[kGroup * 64 * 64 + hq * 64 + lane] = m_run;
     part[kGroup * 64 * 65 + hq * 64 + lane] = l_run;
   }
@@ -811,11 +843,11 @@ triangle_paged_attention_combine_kernel(KernelParams p) {
   }
 }
 
-template <bool kSparse>
+template <bool kSparse, int P>
 hipError_t launch(const KernelParams& p, bool any_split, hipStream_t stream) {
-  hipLaunchKernelGGL(triangle_paged_attention_kernel<kSparse>,
-                     dim3((unsigned)(p.items_per_head * kGroupsPerKvHead * kKvHeads)), dim3(kThreads), 0, stream,
-                     p);
+  hipLaunchKernelGGL((triangle_paged_attention_kernel<kSparse, P>),
+                     dim3((unsigned)(p.items_per_head * Shape<P>::kWgPerKvHead * kKvHeads)), dim3(kThreads), 0,
+                     stream, p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !any_split) return err;
   hipLaunchKernelGGL(triangle_paged_attention_combine_kernel<kSparse>,
@@ -823,8 +855,10 @@ hipError_t launch(const KernelParams& p, bool any_split, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, bool any_split, hipStream_t stream) {
-  return sparse ? launch<true>(p, any_split, stream) : launch<false>(p, any_split, stream);
+hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, bool any_split, int kv_parts,
+                                           hipStream_t stream) {
+  if (kv_parts == 2) return sparse ? launch<true, 2>(p, any_split, stream) : launch<false, 2>(p, any_split, stream);
+  return sparse ? launch<true, 4>(p, any_split, stream) : launch<false, 4>(p, any_split, stream);
 }
 
 }  // namespace tmx

@@ -1,0 +1,89 @@
+"""Chunks of at least 32 row blocks (1024 query tokens and up) on the GPU.
+
+Such chunks run a different workgroup shape from shorter ones: the four
+query heads of a GQA group per workgroup and the item's K/V tiles cut into
+two halves (instead of two heads and four quarters).  These cases pin that
+shape against the fp32 oracle: the first chunk of a prompt (dense prefix,
+sparse start), the shape boundary at 992 / 993 / 1024 query tokens, ragged
+and mid-page chunks, long chunks whose dense tail splits over KV, a chunk
+whose prompt extends past the sequence (no dense tail yet), 32-row blocks
+that hold a single live row, and the dense companion.  Tolerances are the
+project's (max-abs 2e-2, mean-abs 2e-3, relative L2 2e-2 vs fp32).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import attention as OA
+from trianglemix import cabi
+from trianglemix.workload import SCALE, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS, REL_L2 = 2e-2, 2e-3, 2e-2
+HALVES_MIN_ROW_BLOCKS = 32  # chunks of at least this many 32-row blocks take the KV-halves shape
+
+# (name, query_start, query_tokens, seq_len, prompt_len, seed)
+CASES = [
+    ("first_chunk_1024", 0, 1024, 1024, 8192, 71),
+    ("quarters_side_992", 1000, 992, 1992, 4000, 72),
+    ("halves_side_993_one_live_row", 1000, 993, 1993, 4000, 73),
+    ("ragged_1057_mid_page", 1333, 1057, 2390, 2390, 74),
+    ("chunk_2048_no_tail_yet", 2048, 2048, 4096, 8192, 75),
+    ("last_chunk_1024_split_tail", 7168, 1024, 8192, 8192, 76),
+    ("last_chunk_2048_16k_split_tail", 14336, 2048, 16384, 16384, 77),
+    ("whole_prompt_1500", 0, 1500, 1500, 1500, 78),
+    ("prompt_past_sequence_1111", 3000, 1111, 4111, 9000, 79),
+]
+
+
+def _row_blocks(tq: int) -> int:
+    return (tq + 31) // 32
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_kv_halves_matches_oracle(gpu, case):
+    name, qs, tq, seq, prompt, seed = case
+    print(f"case {name} qs={qs} tq={tq} seq={seq} prompt={prompt} row_blocks={_row_blocks(tq)}", flush=True)
+    q, k, v, bt = make_inputs(qs, tq, seq, seed, std=1.0)
+    qd, kd, vd, btd = q.to(gpu), k.to(gpu), v.to(gpu), bt.to(gpu)
+    out = torch.full_like(qd, float("nan"))
+    cabi.triangle_paged_sparse_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, prompt_len=prompt,
+                                         scale=SCALE)
+    torch.cuda.synchronize()
+    expected = OA.attention_torch(q, k, v, bt, qs, seq, prompt, SCALE)
+    m = OA.error_metrics(out.float().cpu().numpy(), expected.float().numpy())
+    print(f"{name}: {m}", flush=True)
+    assert m["finite"] and m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS and m["relative_l2"] <= REL_L2, m
+
+
+@pytest.mark.parametrize("qs,tq,seq", [(0, 1024, 1024), (1900, 1100, 3000), (5000, 2048, 7048)])
+def test_kv_halves_dense_companion(gpu, qs, tq, seq):
+    assert _row_blocks(tq) >= HALVES_MIN_ROW_BLOCKS
+    print(f"dense qs={qs} tq={tq} seq={seq}", flush=True)
+    q, k, v, bt = make_inputs(qs, tq, seq, 900 + tq, std=1.0)
+    qd, kd, vd, btd = q.to(gpu), k.to(gpu), v.to(gpu), bt.to(gpu)
+    out = torch.full_like(qd, float("nan"))
+    cabi.dense_paged_causal_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, scale=SCALE)
+    torch.cuda.synchronize()
+    expected = OA.attention_torch(q, k, v, bt, qs, seq, seq, SCALE, dense=True)
+    m = OA.error_metrics(out.float().cpu().numpy(), expected.float().numpy())
+    print(f"dense {qs}+{tq}: {m}", flush=True)
+    assert m["finite"] and m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS and m["relative_l2"] <= REL_L2, m
+
+
+def test_kv_halves_deterministic_across_calls(gpu):
+    """Two launches of one split chunk give identical bytes (fixed merge order)."""
+    qs, tq, seq, prompt = 7168, 1024, 8192, 8192
+    q, k, v, bt = make_inputs(qs, tq, seq, 81, std=1.0)
+    qd, kd, vd, btd = q.to(gpu), k.to(gpu), v.to(gpu), bt.to(gpu)
+    a = torch.full_like(qd, float("nan"))
+    b = torch.full_like(qd, float("nan"))
+    for out in (a, b):
+        cabi.triangle_paged_sparse_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, prompt_len=prompt,
+                                             scale=SCALE)
+    torch.cuda.synchronize()
+    assert torch.isfinite(a.float()).all()
+    assert torch.equal(a, b)
