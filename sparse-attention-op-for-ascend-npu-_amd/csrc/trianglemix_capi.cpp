@@ -56,15 +56,20 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
   return TM_OK;
 }
 
-// Workgroup shape.  Chunks of at least kHalvesMinRowBlocks row blocks run
-// with KV halves (the four heads of a GQA group per workgroup, 8 workgroups
-// per work item): their 8 x row blocks workgroups still cover the 256 CUs,
-// each K/V tile then serves four heads, and a sparse row block's 18 tiles
-// split evenly.  Smaller chunks run with KV quarters (two heads per
-// workgroup, 16 workgroups per item) to fill the CUs.
-constexpr int kHalvesMinRowBlocks = 32;
-
-int kv_parts_for(int num_row_blocks) { return num_row_blocks >= kHalvesMinRowBlocks ? 2 : 4; }
+// Workgroup shape.  KV quarters: two query heads per workgroup over four KV
+// parts, 16 workgroups per work item.  KV halves: the four heads of a GQA
+// group over two KV parts, 8 workgroups per item; each K/V tile then serves
+// four heads and a workgroup issues half the DMA and merge work per MFMA.
+// Halves run every chunk of more than 16 row blocks (16 x row blocks quarter
+// workgroups would exceed the 256 CUs, 8 x row blocks halves ones do not up
+// to 32), and chunks of at least 4 row blocks whose halves plan splits a row
+// block over KV (long dense rows: the splits fill the CUs either way).  The
+// thresholds are measured on MI355X: unsplit chunks of up to 16 row blocks
+// run 15-25 % faster as quarters, split chunks of 4 row blocks and more
+// 3-16 % faster as halves, split chunks of 1-2 row blocks a few % faster as
+// quarters.
+constexpr int kHalvesMinRowBlocks = 17;
+constexpr int kHalvesSplitMinRowBlocks = 4;
 
 // Split-KV sizing.  A work item runs as 16 (KV quarters) or 8 (KV halves)
 // workgroups, one per CU, so each of the item's workgroup positions has
@@ -87,7 +92,6 @@ struct PlanCosts {
 constexpr PlanCosts kQuarterCosts{16, 15, 15};
 constexpr PlanCosts kHalfCosts{32, 8, 8};
 constexpr int kMaxSlots = 32;
-PlanCosts plan_costs(int kv_parts) { return kv_parts == 2 ? kHalfCosts : kQuarterCosts; }
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 // Beyond this many items per candidate the simulation is skipped (its host
 // cost would show): T then spreads the chunk's tiles over one item per slot.
@@ -146,10 +150,26 @@ struct PlanKey {
   }
 };
 
-int cached_tiles_per_split(const PlanKey& key) {
+struct ChunkPlan {
+  int kv_parts, tiles_per_split;
+};
+
+ChunkPlan choose_plan(const std::vector<int>& row_tiles) {
+  const int num_row_blocks = (int)row_tiles.size();
+  const int t_halves = choose_tiles_per_split(row_tiles, kHalfCosts);
+  if (num_row_blocks >= kHalvesMinRowBlocks) return {2, t_halves};
+  if (num_row_blocks >= kHalvesSplitMinRowBlocks) {
+    for (const int n : row_tiles) {
+      if (n > t_halves) return {2, t_halves};
+    }
+  }
+  return {4, choose_tiles_per_split(row_tiles, kQuarterCosts)};
+}
+
+ChunkPlan cached_plan(const PlanKey& key) {
   constexpr int kEntries = 8;
   thread_local PlanKey keys[kEntries];
-  thread_local int values[kEntries];
+  thread_local ChunkPlan values[kEntries];
   thread_local int used = 0, next = 0;
   for (int i = 0; i < used; ++i) {
     if (keys[i] == key) return values[i];
@@ -159,12 +179,12 @@ int cached_tiles_per_split(const PlanKey& key) {
     row_tiles[(size_t)o] = tmx::row_block_splits((int)o, (int)key.num_row_blocks, (int)key.query_start,
                                                  (int)key.seq_len, (int)key.sparse_begin, (int)key.sparse_end, 1);
   }
-  const int t = choose_tiles_per_split(row_tiles, plan_costs(kv_parts_for((int)key.num_row_blocks)));
+  const ChunkPlan plan = choose_plan(row_tiles);
   keys[next] = key;
-  values[next] = t;
+  values[next] = plan;
   next = (next + 1) % kEntries;
   used = used < kEntries ? used + 1 : used;
-  return t;
+  return plan;
 }
 
 // Work items per KV head beyond which a launch is refused (its grid would
@@ -183,9 +203,9 @@ Geometry make_geometry(bool sparse, int64_t query_tokens, int64_t query_start, i
   g.sparse_begin = sparse ? tmx::kSparseBegin : 0;
   g.sparse_end = sparse ? (int)(prompt_len > tmx::kDenseTail ? prompt_len - tmx::kDenseTail : 0) : 0;
   g.num_row_blocks = (int)((query_tokens + tmx::kRowBlock - 1) / tmx::kRowBlock);
-  g.kv_parts = kv_parts_for(g.num_row_blocks);
-  g.tiles_per_split = cached_tiles_per_split(
-      PlanKey{g.num_row_blocks, query_start, seq_len, g.sparse_begin, g.sparse_end});
+  const ChunkPlan plan = cached_plan(PlanKey{g.num_row_blocks, query_start, seq_len, g.sparse_begin, g.sparse_end});
+  g.kv_parts = plan.kv_parts;
+  g.tiles_per_split = plan.tiles_per_split;
   bool any_split = false;
   int64_t items = 0;
   for (int o = 0; o < g.num_row_blocks; ++o) {

@@ -2,16 +2,20 @@
 //
 // Work decomposition
 // ------------------
-// A work item is (row block of 32 query tokens, KV head, KV split); each item
-// runs as two workgroups, one per pair of the KV head's four GQA query heads.
-// A workgroup has eight wave64s, two per SIMD: (query head hl of the pair) x
-// (KV quarter kq).  Wave w owns the 32 rows {32 tokens} x {head 4*kvh + 2*hp +
-// hl} and processes every fourth 32-key tile of the item (tiles kq, kq+4,
-// ...); each K/V tile staged in LDS is read by the two waves of its quarter,
-// and the four quarters merge through LDS at the end.  Splitting the GQA group
-// over two workgroups puts 256 workgroups on the 256 CUs for a 512-token
-// chunk; two waves per SIMD let one wave's softmax run while the other's
-// MFMAs occupy the matrix core.
+// A work item is (row block of 32 query tokens, KV head, KV split).  A
+// workgroup has eight wave64s, two per SIMD: (query head hl) x (KV part kq),
+// in one of two shapes (template parameter P, chosen per chunk by the host):
+//  * P = 4, KV quarters: each item runs as two workgroups, one per pair of the
+//    KV head's four GQA query heads; wave w owns the 32 rows {32 tokens} x
+//    {head 4*kvh + 2*hp + hl} and processes every fourth 32-key tile of the
+//    item (tiles kq, kq+4, ...).  A 512-token chunk fills the 256 CUs.
+//  * P = 2, KV halves: one workgroup holds all four heads of the group and
+//    every wave every second tile; each K/V tile then serves four heads, so a
+//    workgroup issues half the DMA per MFMA -- for chunks with enough row
+//    blocks (or split items) to fill the CUs anyway.
+// Each K/V tile staged in LDS is read by the waves of its part, and the parts
+// merge through LDS at the end.  Two waves per SIMD let one wave's softmax
+// run while the other's MFMAs occupy the matrix core.
 // The KV tiles of a row block are cut into splits of at most
 // `tiles_per_split` tiles (host-chosen: at least 1024 keys, at most
 // kMaxItemTiles tiles), so only long dense rows split.  A row block with one
@@ -23,8 +27,8 @@
 // Items are numbered per KV head, heaviest row blocks first; KV head =
 // blockIdx % 8 keeps every workgroup of one KV head on one XCD (workgroups
 // are dispatched round-robin over the 8 XCDs), so both head pairs of a row
-// block, neighbouring row blocks' overlapping local windows and a row block's
-// partials share one L2.
+// block (KV quarters), neighbouring row blocks' overlapping local windows and
+// a row block's partials share one L2.
 //
 // Tiles, memory path and pipeline
 // -------------------------------
@@ -36,10 +40,10 @@
 // tile of iteration i, then the PV MFMAs of tile i interleaved with the mask
 // and row max of tile i+1 (the interleave is fixed in program order with
 // scheduling barriers).  LDS holds two K slots and two V slots, each with the
-// four tiles (one per quarter) of one iteration, plus the workgroup's Q (DMA'd
+// P tiles (one per part) of one iteration, plus the workgroup's Q (DMA'd
 // once, read into registers in the prologue); the DMA of K for iteration
 // i+2 (waves 0-3) and of V for iteration i+1 (waves 4-7) is spread over the
-// MFMA steps of iteration i, one instruction per step.  The four slots are
+// MFMA steps of iteration i.  The four slots are
 // distinct LDS objects and the loop is unrolled by two so every access names
 // its slot statically: the compiler then sees that the prefetch never aliases
 // the tiles being read and does not wait for it.  Each wave waits for its own
@@ -80,7 +84,7 @@
 // block_epilogue_rescale_o.hpp:153-344): s*scale -> mask -> row max -> p = exp(s - m) in
 // fp32 -> P to bf16 (round to nearest even) for PV, row sum from the fp32 p
 // -> O = O*exp(m_old - m_new) + P V -> O / l -> bf16 round to nearest even.
-// Exponentials are exp2 of log2(e)-prescaled scores; the KV quarters and the
+// Exponentials are exp2 of log2(e)-prescaled scores; the KV parts and the
 // split partials merge with the same rescale rule.
 
 #include <hip/hip_runtime.h>
@@ -542,7 +546,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     wait_dma();
     __syncthreads();  // DMA issued one iteration ago landed; slots kw / vw are no longer read
     const int ti = P * it + kq;
-    // Ragged last iteration: the quarters without a tile idle; nothing is
+    // Ragged last iteration: the parts without a tile idle; nothing is
     // left to prefetch in the last iteration.
     if (ti >= num_tiles) return;
     // This wave's prefetch: K of iteration it+2 (waves 0-3) or V of it+1

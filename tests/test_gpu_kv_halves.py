@@ -1,14 +1,17 @@
-"""Chunks of at least 32 row blocks (1024 query tokens and up) on the GPU.
+"""The KV-halves workgroup shape on the GPU.
 
-Such chunks run a different workgroup shape from shorter ones: the four
-query heads of a GQA group per workgroup and the item's K/V tiles cut into
-two halves (instead of two heads and four quarters).  These cases pin that
-shape against the fp32 oracle: the first chunk of a prompt (dense prefix,
-sparse start), the shape boundary at 992 / 993 / 1024 query tokens, ragged
-and mid-page chunks, long chunks whose dense tail splits over KV, a chunk
-whose prompt extends past the sequence (no dense tail yet), 32-row blocks
-that hold a single live row, and the dense companion.  Tolerances are the
-project's (max-abs 2e-2, mean-abs 2e-3, relative L2 2e-2 vs fp32).
+Chunks of more than 16 row blocks (513 query tokens and up), and chunks of
+at least 4 row blocks whose long dense rows split over KV, run a different
+workgroup shape from the others: the four query heads of a GQA group per
+workgroup and the item's K/V tiles cut into two halves (instead of two heads
+and four quarters).  These cases pin that shape against the fp32 oracle: the
+first chunk of a prompt (dense prefix, sparse start), the shape boundary at
+512 / 513 query tokens, ragged and mid-page chunks, long chunks whose dense
+tail splits over KV, short split chunks on either side of the 4-row-block
+bound, a chunk whose prompt extends past the sequence (no dense tail yet),
+32-row blocks that hold a single live row, and the dense companion.
+Tolerances are the project's (max-abs 2e-2, mean-abs 2e-3, relative L2 2e-2
+vs fp32).
 """
 
 from __future__ import annotations
@@ -23,13 +26,17 @@ from trianglemix.workload import SCALE, make_inputs
 pytestmark = pytest.mark.gpu
 
 MAX_ABS, MEAN_ABS, REL_L2 = 2e-2, 2e-3, 2e-2
-HALVES_MIN_ROW_BLOCKS = 32  # chunks of at least this many 32-row blocks take the KV-halves shape
+HALVES_MIN_ROW_BLOCKS = 17  # chunks of at least this many 32-row blocks take the KV-halves shape
 
 # (name, query_start, query_tokens, seq_len, prompt_len, seed)
 CASES = [
     ("first_chunk_1024", 0, 1024, 1024, 8192, 71),
-    ("quarters_side_992", 1000, 992, 1992, 4000, 72),
-    ("halves_side_993_one_live_row", 1000, 993, 1993, 4000, 73),
+    ("quarters_side_512", 1000, 512, 1512, 4000, 72),
+    ("halves_side_513_one_live_row", 1000, 513, 1513, 4000, 73),
+    ("halves_993_one_live_row", 1000, 993, 1993, 4000, 80),
+    ("split_tail_3_row_blocks_quarters", 12200, 96, 12296, 12296, 82),
+    ("split_tail_4_row_blocks_halves", 12200, 128, 12328, 12328, 83),
+    ("split_tail_8_row_blocks_halves", 8000, 256, 8256, 8256, 84),
     ("ragged_1057_mid_page", 1333, 1057, 2390, 2390, 74),
     ("chunk_2048_no_tail_yet", 2048, 2048, 4096, 8192, 75),
     ("last_chunk_1024_split_tail", 7168, 1024, 8192, 8192, 76),
@@ -59,7 +66,7 @@ def test_kv_halves_matches_oracle(gpu, case):
     assert m["finite"] and m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS and m["relative_l2"] <= REL_L2, m
 
 
-@pytest.mark.parametrize("qs,tq,seq", [(0, 1024, 1024), (1900, 1100, 3000), (5000, 2048, 7048)])
+@pytest.mark.parametrize("qs,tq,seq", [(0, 1024, 1024), (1900, 1100, 3000), (5000, 2048, 7048), (0, 600, 600)])
 def test_kv_halves_dense_companion(gpu, qs, tq, seq):
     assert _row_blocks(tq) >= HALVES_MIN_ROW_BLOCKS
     print(f"dense qs={qs} tq={tq} seq={seq}", flush=True)
