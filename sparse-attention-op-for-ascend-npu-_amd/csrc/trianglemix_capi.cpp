@@ -78,19 +78,25 @@ constexpr int kHalvesSplitMinRowBlocks = 4;
 // the greedy dispatch of the items (issued heaviest row block first) onto the
 // slots, an item costing a fixed start-up + merge + store cost plus its tiles,
 // and taking the T with the shortest makespan (ties: larger T, fewer
-// partials); a plan that splits anything also pays for the combine kernel.
-// Costs are in tile times: a KV-halves workgroup runs a tile per part and
-// iteration as a quarters one does, but over two parts, so its fixed costs
-// weigh half as many tile times.  T is at least kMinSplitTiles (1024 keys: a
+// partials); a plan that splits anything also pays for the combine kernel
+// and, per split item, for its fp32 partial (written, then read back by the
+// combine kernel).  Costs are in tile times: a KV-halves workgroup runs a tile
+// per part and iteration as a quarters one does, but over two parts.  The
+// halves costs are fitted to a forced-T sweep on MI355X: over nine split
+// chunks of 128-2048 rows (prompts 2869-16384) they pick the fastest measured
+// split on all nine.  The previous costs, fixed 8 and no per-split term
+// (half the quarters' fixed cost), lost 17.7 us summed over those chunks.
+// They split 1024-2048-row chunks into up to twice the items, 4-15 % slower.  T is at least kMinSplitTiles (1024 keys: a
 // split's fp32 partial of 66 KB stays small next to the K/V it reads, 16 KB
 // per 32-key tile) and at most kMaxItemTiles.
 struct PlanCosts {
   int slots;
-  int item_fixed_tiles;  // start-up, merge and store of an item (measured)
-  int combine_tiles;     // the combine kernel a plan with splits adds (measured)
+  int item_fixed_tiles;  // start-up, merge and store of an item
+  int combine_tiles;     // the combine kernel a plan with splits adds
+  int split_item_tiles;  // each item of a split row block
 };
-constexpr PlanCosts kQuarterCosts{16, 15, 15};
-constexpr PlanCosts kHalfCosts{32, 8, 8};
+constexpr PlanCosts kQuarterCosts{16, 15, 15, 0};  // measured
+constexpr PlanCosts kHalfCosts{32, 12, 8, 1};     // fitted
 constexpr int kMaxSlots = 32;
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 // Beyond this many items per candidate the simulation is skipped (its host
@@ -100,8 +106,10 @@ constexpr int kSplitStep = 4;  // candidate T: kMaxItemTiles, kMaxItemTiles - 4,
 
 int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanCosts& c) {
   int64_t slot[kMaxSlots] = {};
+  int64_t split_items = 0;
   for (const int n : row_tiles) {
     const int pieces = (n + T - 1) / T;
+    split_items += pieces > 1 ? pieces : 0;
     for (int i = 0; i < pieces; ++i) {
       const int size = (int)((int64_t)(i + 1) * n / pieces - (int64_t)i * n / pieces);
       int best = 0;
@@ -110,10 +118,8 @@ int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanC
     }
   }
   int64_t makespan = 0;
-  bool any_split = false;
   for (int k = 0; k < c.slots; ++k) makespan = slot[k] > makespan ? slot[k] : makespan;
-  for (const int n : row_tiles) any_split = any_split || n > T;
-  return makespan + (any_split ? c.combine_tiles : 0);
+  return makespan + (split_items > 0 ? c.combine_tiles + c.split_item_tiles * split_items : 0);
 }
 
 int choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c) {
