@@ -244,3 +244,30 @@ def test_cpu_tensors_have_no_kernel(adapter):
     kv = torch.zeros(4, 8, 128, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
         adapter.trianglemix.reshape_and_cache(kv, kv, k, k.clone(), torch.zeros(4, dtype=torch.int64))
+
+
+# (query_start, query_tokens, seq_len, prompt_len) -> work items per KV head.
+# Each count is the split of the fastest measured plan on MI355X: every chunk
+# was timed at 8-12 forced tiles-per-split values, and the planner's cost
+# model (KV halves: fixed 12 tile times per item, combine 8, 1 per split item;
+# KV quarters: 15 / 15 / 0) was fitted until it picks that split for all of
+# them.  The last one runs as KV quarters (3 row blocks), the rest as halves.
+FASTEST_MEASURED_SPLITS = [
+    ((2357, 512, 2869, 2869), 24),      # config 1: 12 sparse items + 4 tail rows x 3
+    ((7680, 512, 8192, 8192), 32),      # config 2, last chunk: 12 + 4 x 5
+    ((6272, 2048, 8320, 8320), 72),
+    ((16128, 256, 16384, 16384), 32),   # 8 tail rows x 4
+    ((14336, 2048, 16384, 16384), 76),
+    ((8192, 128, 8320, 8320), 32),      # config 3, last chunk: 4 tail rows x 8
+    ((15360, 1024, 16384, 16384), 48),
+    ((7168, 1024, 8192, 8192), 44),
+    ((3584, 512, 4096, 4096), 28),
+    ((12288, 96, 12384, 12384), 15),
+]
+
+
+@pytest.mark.parametrize("geom,items", FASTEST_MEASURED_SPLITS, ids=[str(g[0]) for g in FASTEST_MEASURED_SPLITS])
+def test_split_plan_is_the_fastest_measured(lib, geom, items):
+    qs, tq, seq, prompt = geom
+    need = lib.tm_triangle_paged_sparse_attention_workspace_size(tq, qs, seq, prompt)
+    assert need == 8 * items * PARTIAL_BYTES, (geom, need / (8 * PARTIAL_BYTES))
