@@ -63,13 +63,21 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
 // Halves run every chunk of more than 16 row blocks (16 x row blocks quarter
 // workgroups would exceed the 256 CUs, 8 x row blocks halves ones do not up
 // to 32), and chunks of at least 4 row blocks whose halves plan splits a row
-// block over KV (long dense rows: the splits fill the CUs either way).  The
-// thresholds are measured on MI355X: unsplit chunks of up to 16 row blocks
-// run 15-25 % faster as quarters, split chunks of 4 row blocks and more
-// 3-16 % faster as halves, split chunks of 1-2 row blocks a few % faster as
-// quarters.
+// block over KV -- for the dense companion only when the chunk also holds at
+// least kHalvesDenseMinTiles tiles per KV head.  The thresholds are measured
+// on MI355X:
+//  * unsplit chunks of up to 16 row blocks run 15-25 % faster as quarters;
+//  * split TriangleMix chunks (a prompt's last chunk, whose dense tail rows
+//    split) of 4 row blocks and more run 3-16 % faster as halves, and those
+//    of 1-2 row blocks a few % faster as quarters;
+//  * dense-companion chunks of up to 16 row blocks, whose rows all split, run
+//    faster as halves only with enough work: over whole prefills in chunks of
+//    128-512 (L = 4096-16384) the tile bound is the fastest rule or within
+//    1 % of it, against up to 9 % slower for halves on every split chunk and
+//    up to 12 % slower for quarters on every one.
 constexpr int kHalvesMinRowBlocks = 17;
 constexpr int kHalvesSplitMinRowBlocks = 4;
+constexpr int64_t kHalvesDenseMinTiles = 2048;
 
 // Split-KV sizing.  A work item runs as 16 (KV quarters) or 8 (KV halves)
 // workgroups, one per CU, so each of the item's workgroup positions has
@@ -160,14 +168,18 @@ struct ChunkPlan {
   int kv_parts, tiles_per_split;
 };
 
-ChunkPlan choose_plan(const std::vector<int>& row_tiles) {
+ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
   const int num_row_blocks = (int)row_tiles.size();
   const int t_halves = choose_tiles_per_split(row_tiles, kHalfCosts);
   if (num_row_blocks >= kHalvesMinRowBlocks) return {2, t_halves};
   if (num_row_blocks >= kHalvesSplitMinRowBlocks) {
+    int64_t total = 0;
+    bool split = false;
     for (const int n : row_tiles) {
-      if (n > t_halves) return {2, t_halves};
+      total += n;
+      split = split || n > t_halves;
     }
+    if (split && (sparse || total >= kHalvesDenseMinTiles)) return {2, t_halves};
   }
   return {4, choose_tiles_per_split(row_tiles, kQuarterCosts)};
 }
@@ -185,7 +197,7 @@ ChunkPlan cached_plan(const PlanKey& key) {
     row_tiles[(size_t)o] = tmx::row_block_splits((int)o, (int)key.num_row_blocks, (int)key.query_start,
                                                  (int)key.seq_len, (int)key.sparse_begin, (int)key.sparse_end, 1);
   }
-  const ChunkPlan plan = choose_plan(row_tiles);
+  const ChunkPlan plan = choose_plan(row_tiles, key.sparse_begin != 0);  // 0 only for the dense companion
   keys[next] = key;
   values[next] = plan;
   next = (next + 1) % kEntries;
