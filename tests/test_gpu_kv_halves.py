@@ -94,3 +94,28 @@ def test_kv_halves_deterministic_across_calls(gpu):
     torch.cuda.synchronize()
     assert torch.isfinite(a.float()).all()
     assert torch.equal(a, b)
+
+
+# Dense-companion chunks of at most 16 row blocks whose rows all split: KV
+# halves once the chunk holds at least 2048 tiles per KV head, KV quarters
+# below that.
+DENSE_SPLIT_CASES = [
+    (7680, 512, 8192),    # 16 row blocks, ~3970 tiles: halves
+    (12000, 256, 12256),  # 8 row blocks, ~3040 tiles: halves
+    (12200, 128, 12328),  # 4 row blocks, ~1540 tiles: quarters
+    (5000, 512, 5512),    # 16 row blocks, ~2650 tiles: halves
+]
+
+
+@pytest.mark.parametrize("qs,tq,seq", DENSE_SPLIT_CASES)
+def test_dense_split_chunks_either_shape(gpu, qs, tq, seq):
+    print(f"dense split qs={qs} tq={tq} seq={seq} row_blocks={_row_blocks(tq)}", flush=True)
+    q, k, v, bt = make_inputs(qs, tq, seq, 700 + tq, std=1.0)
+    qd, kd, vd, btd = q.to(gpu), k.to(gpu), v.to(gpu), bt.to(gpu)
+    out = torch.full_like(qd, float("nan"))
+    cabi.dense_paged_causal_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, scale=SCALE)
+    torch.cuda.synchronize()
+    expected = OA.attention_torch(q, k, v, bt, qs, seq, seq, SCALE, dense=True)
+    m = OA.error_metrics(out.float().cpu().numpy(), expected.float().numpy())
+    print(f"dense split {qs}+{tq}: {m}", flush=True)
+    assert m["finite"] and m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS and m["relative_l2"] <= REL_L2, m
