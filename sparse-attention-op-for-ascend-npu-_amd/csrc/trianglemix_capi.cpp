@@ -106,6 +106,7 @@ struct PlanCosts {
 constexpr PlanCosts kQuarterCosts{16, 15, 15, 0};  // measured
 constexpr PlanCosts kHalfCosts{32, 12, 8, 1};     // fitted
 constexpr int kMaxSlots = 32;
+static_assert(kQuarterCosts.slots <= kMaxSlots && kHalfCosts.slots <= kMaxSlots, "simulated_makespan's slot array");
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 // Beyond this many items per candidate the simulation is skipped (its host
 // cost would show): T then spreads the chunk's tiles over one item per slot.

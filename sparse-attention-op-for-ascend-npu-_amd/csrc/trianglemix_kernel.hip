@@ -89,7 +89,6 @@
 
 #include <hip/hip_runtime.h>
 
-#include <type_traits>
 #include <stdint.h>
 
 #include "trianglemix_kernel.h"
@@ -336,6 +335,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   const int dma_u = dma_tile % P;  // part
   const int dma_j0 = (wave % S::kWavesPerTile) * S::kDmaPerWave;  // this wave's first instruction of the tile
   unsigned dma_voff[kDmaPerTile];  // the first kDmaPerWave are used (fixed size: see kept below)
+  static_assert(S::kDmaPerWave <= kDmaPerTile, "dma_voff holds one tile's instructions");
 #pragma unroll
   for (int j = 0; j < S::kDmaPerWave; ++j) {
     const int row = 4 * (dma_j0 + j) + (lane >> 4);
@@ -673,6 +673,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   // size (the largest shape's): hipcc's host pass drops a kernel template
   // whose local arrays have a size that depends on the template parameters.
   f32x16_t kept[kHeadDim / 32 / 2];
+  static_assert(O <= kHeadDim / 32 / 2 && P <= 4, "kept, mq and lq hold the largest shape's blocks");
   {
     float mq[4], lq[4];  // the first P are used
     float mt = -INFINITY;
