@@ -806,11 +806,11 @@ triangle_paged_attention_combine_kernel(KernelParams p) {
   const int m_off = kGroup * 64 * 64 + hq * 64 + lane;  // row max of this lane's row
   const int l_off = kGroup * 64 * 65 + hq * 64 + lane;  // this lane's partial row sum
 
+  // One pass over the splits, eight at a time: the running max mt rescales
+  // what is already summed when a batch raises it (the online-softmax rule),
+  // so the row maxima need no round trip of their own.  Splits are summed in
+  // order (deterministic).
   float mt = -INFINITY;
-#pragma unroll 8
-  for (int s = 0; s < nsplit; ++s) mt = fmaxf(mt, base[(size_t)s * kPartialFloats + m_off]);
-  const float mu = mt == -INFINITY ? 0.0f : mt;
-
   float lt = 0.0f;
   f32x4_t ot[4] = {};  // [v/4] of d-block m, 4 consecutive v each
   for (int s0 = 0; s0 < nsplit; s0 += kCombineBatch) {
@@ -827,6 +827,14 @@ triangle_paged_attention_combine_kernel(KernelParams p) {
       w[b] = part[m_off];
       ls[b] = part[l_off];
     }
+    float mb = mt;
+#pragma unroll
+    for (int b = 0; b < kCombineBatch; ++b) mb = s0 + b < nsplit ? fmaxf(mb, w[b]) : mb;
+    const float mu = mb == -INFINITY ? 0.0f : mb;  // all maxima so far -inf: nothing is summed yet
+    const float keep = mt == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mt - mu);
+    lt *= keep;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) ot[g] *= keep;
 #pragma unroll
     for (int b = 0; b < kCombineBatch; ++b) {
       const float wb = s0 + b < nsplit ? __builtin_amdgcn_exp2f(w[b] - mu) : 0.0f;
@@ -834,6 +842,7 @@ triangle_paged_attention_combine_kernel(KernelParams p) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) ot[g] += os[b][g] * wb;
     }
+    mt = mb;
   }
   const float l_tot = half_sum(lt);  // the two 32-lane halves hold one row
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
