@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -68,8 +69,11 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
 // on MI355X:
 //  * unsplit chunks of up to 16 row blocks run 15-25 % faster as quarters;
 //  * split TriangleMix chunks (a prompt's last chunk, whose dense tail rows
-//    split) of 4 row blocks and more run 3-16 % faster as halves, and those
-//    of 1-2 row blocks a few % faster as quarters;
+//    split) of 4 row blocks and more mostly run 3-16 % faster as halves, and
+//    those of 1-3 row blocks a few % faster as quarters; quarters still win
+//    when their plan fits one round of workgroups with shorter items (the
+//    iteration test in choose_plan), e.g. the last chunk of a 2048-token
+//    prompt (20.6 against 23.9 us);
 //  * dense-companion chunks of up to 16 row blocks, whose rows all split, run
 //    faster as halves only with enough work: over whole prefills in chunks of
 //    128-512 (L = 4096-16384) the tile bound is the fastest rule or within
@@ -180,7 +184,29 @@ ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
       total += n;
       split = split || n > t_halves;
     }
-    if (split && (sparse || total >= kHalvesDenseMinTiles)) return {2, t_halves};
+    if (split && !sparse && total >= kHalvesDenseMinTiles) return {2, t_halves};
+    if (split && sparse) {
+      // Quarters keep a split TriangleMix chunk when their plan fits one round
+      // of workgroups and its longest item needs fewer loop iterations (4
+      // tiles each) than the halves plan's (2 tiles each) -- or as many
+      // without any split, which saves the combine kernel.
+      const int t_quarters = choose_tiles_per_split(row_tiles, kQuarterCosts);
+      int64_t q_items = 0;
+      int q_iters = 0, h_iters = 0;
+      bool q_split = false;
+      for (const int n : row_tiles) {
+        const int qp = (n + t_quarters - 1) / t_quarters;
+        const int hp = (n + t_halves - 1) / t_halves;
+        q_items += qp;
+        q_split = q_split || qp > 1;
+        q_iters = std::max(q_iters, ((n + qp - 1) / qp + 3) / 4);
+        h_iters = std::max(h_iters, ((n + hp - 1) / hp + 1) / 2);
+      }
+      if (q_items <= kQuarterCosts.slots && (q_iters < h_iters || (q_iters == h_iters && !q_split))) {
+        return {4, t_quarters};
+      }
+      return {2, t_halves};
+    }
   }
   return {4, choose_tiles_per_split(row_tiles, kQuarterCosts)};
 }

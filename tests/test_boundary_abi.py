@@ -251,7 +251,7 @@ def test_cpu_tensors_have_no_kernel(adapter):
 # was timed at 8-12 forced tiles-per-split values, and the planner's cost
 # model (KV halves: fixed 12 tile times per item, combine 8, 1 per split item;
 # KV quarters: 15 / 15 / 0) was fitted until it picks that split for all of
-# them.  The last one runs as KV quarters (3 row blocks), the rest as halves.
+# them.  The last three run as KV quarters, the rest as halves.
 FASTEST_MEASURED_SPLITS = [
     ((2357, 512, 2869, 2869), 24),      # config 1: 12 sparse items + 4 tail rows x 3
     ((7680, 512, 8192, 8192), 32),      # config 2, last chunk: 12 + 4 x 5
@@ -263,6 +263,8 @@ FASTEST_MEASURED_SPLITS = [
     ((7168, 1024, 8192, 8192), 44),
     ((3584, 512, 4096, 4096), 28),
     ((12288, 96, 12384, 12384), 15),
+    ((1536, 512, 2048, 2048), 0),       # quarters, no split: 20.6 us against 23.9 as halves
+    ((2560, 309, 2869, 2869), 15),      # quarters in one round: 23.3 us against 25.5 as halves
 ]
 
 
@@ -270,4 +272,4 @@ FASTEST_MEASURED_SPLITS = [
 def test_split_plan_is_the_fastest_measured(lib, geom, items):
     qs, tq, seq, prompt = geom
     need = lib.tm_triangle_paged_sparse_attention_workspace_size(tq, qs, seq, prompt)
-    assert need == 8 * items * PARTIAL_BYTES, (geom, need / (8 * PARTIAL_BYTES))
+    assert need == 8 * items * PARTIAL_BYTES, (geom, need / (8 * PARTIAL_BYTES))  # 0 items: no split, no workspace
