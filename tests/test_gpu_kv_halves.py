@@ -43,6 +43,9 @@ CASES = [
     ("last_chunk_2048_16k_split_tail", 14336, 2048, 16384, 16384, 77),
     ("whole_prompt_1500", 0, 1500, 1500, 1500, 78),
     ("prompt_past_sequence_1111", 3000, 1111, 4111, 9000, 79),
+    # split-candidate chunks that stay KV quarters (one round of workgroups, shorter items)
+    ("quarters_kept_last_chunk_2048_prompt", 1536, 512, 2048, 2048, 85),
+    ("quarters_kept_tail_309_rows", 2560, 309, 2869, 2869, 86),
 ]
 
 
