@@ -273,3 +273,22 @@ def test_split_plan_is_the_fastest_measured(lib, geom, items):
     qs, tq, seq, prompt = geom
     need = lib.tm_triangle_paged_sparse_attention_workspace_size(tq, qs, seq, prompt)
     assert need == 8 * items * PARTIAL_BYTES, (geom, need / (8 * PARTIAL_BYTES))  # 0 items: no split, no workspace
+
+
+# Dense-companion chunks that run as KV quarters: the quarters costs (15 / 15
+# / 0) give the fastest measured split on MI355X for each (forced-T sweep).
+DENSE_FASTEST_MEASURED_SPLITS = [
+    ((3584, 512, 4096), 0),   # rows of up to 128 tiles: unsplit beats every split (41 vs >= 52 us)
+    ((3072, 512, 3584), 0),
+    ((7936, 256, 8192), 16),
+    ((8064, 128, 8192), 16),
+    ((5632, 256, 5888), 16),
+]
+
+
+@pytest.mark.parametrize("geom,items", DENSE_FASTEST_MEASURED_SPLITS,
+                         ids=[str(g[0]) for g in DENSE_FASTEST_MEASURED_SPLITS])
+def test_dense_split_plan_is_the_fastest_measured(lib, geom, items):
+    qs, tq, seq = geom
+    need = lib.tm_dense_paged_causal_attention_workspace_size(tq, qs, seq)
+    assert need == 8 * items * PARTIAL_BYTES, (geom, need / (8 * PARTIAL_BYTES))
