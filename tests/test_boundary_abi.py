@@ -275,14 +275,21 @@ def test_split_plan_is_the_fastest_measured(lib, geom, items):
     assert need == 8 * items * PARTIAL_BYTES, (geom, need / (8 * PARTIAL_BYTES))  # 0 items: no split, no workspace
 
 
-# Dense-companion chunks that run as KV quarters: the quarters costs (15 / 15
-# / 0) give the fastest measured split on MI355X for each (forced-T sweep).
+# Dense-companion chunks: the planner's costs (quarters 15 / 15 / 0, halves
+# 12 / 8 / 1) give the fastest measured split on MI355X for each (forced-T
+# sweep).  The first five run as KV quarters.
 DENSE_FASTEST_MEASURED_SPLITS = [
     ((3584, 512, 4096), 0),   # rows of up to 128 tiles: unsplit beats every split (41 vs >= 52 us)
     ((3072, 512, 3584), 0),
     ((7936, 256, 8192), 16),
     ((8064, 128, 8192), 16),
     ((5632, 256, 5888), 16),
+    # ... and chunks that run as KV halves (above the 2048-tile bound, or over 16 row blocks)
+    ((7680, 512, 8192), 32),
+    ((15872, 512, 16384), 64),
+    ((6144, 2048, 8192), 128),
+    ((4096, 1024, 5120), 64),
+    ((11776, 256, 12032), 32),
 ]
 
 
