@@ -98,9 +98,14 @@ constexpr int64_t kHalvesDenseMinTiles = 2048;
 // chunks of 128-2048 rows (prompts 2869-16384) they pick the fastest measured
 // split on all nine.  The previous costs, fixed 8 and no per-split term
 // (half the quarters' fixed cost), lost 17.7 us summed over those chunks.
-// They split 1024-2048-row chunks into up to twice the items, 4-15 % slower.  T is at least kMinSplitTiles (1024 keys: a
-// split's fp32 partial of 66 KB stays small next to the K/V it reads, 16 KB
-// per 32-key tile) and at most kMaxItemTiles.
+// They split 1024-2048-row chunks into up to twice the items, 4-15 % slower.
+// T is at least kMinSplitTiles (1024 keys: a split's fp32 partial of 66 KB
+// stays small next to the K/V it reads, 16 KB per 32-key tile) and at most
+// kMaxItemTiles.  Split TriangleMix chunks of at most 16 row blocks that run
+// as halves because quarters would need more than one round of workgroups
+// may go down to kFineSplitTiles (768 keys): on five such chunks (prompts
+// 2560-4992, the last 384-512 rows) that plan ran 2-4 % faster, one more
+// piece per dense-tail row while the items still fit the 32 slots.
 struct PlanCosts {
   int slots;
   int item_fixed_tiles;  // start-up, merge and store of an item
@@ -112,10 +117,11 @@ constexpr PlanCosts kHalfCosts{32, 12, 8, 1};     // fitted
 constexpr int kMaxSlots = 32;
 static_assert(kQuarterCosts.slots <= kMaxSlots && kHalfCosts.slots <= kMaxSlots, "simulated_makespan's slot array");
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
+constexpr int kFineSplitTiles = 768 / tmx::kKvTile;
 // Beyond this many items per candidate the simulation is skipped (its host
 // cost would show): T then spreads the chunk's tiles over one item per slot.
 constexpr int64_t kMaxSimulatedItems = 4096;
-constexpr int kSplitStep = 4;  // candidate T: kMaxItemTiles, kMaxItemTiles - 4, ..., >= kMinSplitTiles
+constexpr int kSplitStep = 4;  // candidate T: kMaxItemTiles, kMaxItemTiles - 4, ..., >= the floor
 
 int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanCosts& c) {
   int64_t slot[kMaxSlots] = {};
@@ -135,21 +141,21 @@ int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanC
   return makespan + (split_items > 0 ? c.combine_tiles + c.split_item_tiles * split_items : 0);
 }
 
-int choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c) {
+int choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c, int min_tiles = kMinSplitTiles) {
   int64_t total = 0;
   int longest = 0;
   for (const int n : row_tiles) {
     total += n;
     longest = n > longest ? n : longest;
   }
-  if (longest <= kMinSplitTiles) return kMinSplitTiles;  // nothing to split
-  if (total / kMinSplitTiles > kMaxSimulatedItems) {
+  if (longest <= min_tiles) return min_tiles;  // nothing to split
+  if (total / min_tiles > kMaxSimulatedItems) {
     const int64_t per_item = (total + c.slots - 1) / c.slots;
-    return (int)(per_item < kMinSplitTiles ? kMinSplitTiles : (per_item > tmx::kMaxItemTiles ? tmx::kMaxItemTiles : per_item));
+    return (int)(per_item < min_tiles ? min_tiles : (per_item > tmx::kMaxItemTiles ? tmx::kMaxItemTiles : per_item));
   }
   int best_t = tmx::kMaxItemTiles;
   int64_t best = simulated_makespan(row_tiles, best_t, c);
-  for (int t = tmx::kMaxItemTiles - kSplitStep; t >= kMinSplitTiles; t -= kSplitStep) {
+  for (int t = tmx::kMaxItemTiles - kSplitStep; t >= min_tiles; t -= kSplitStep) {
     const int64_t ms = simulated_makespan(row_tiles, t, c);
     if (ms < best) {
       best = ms;
@@ -205,7 +211,7 @@ ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
       if (q_items <= kQuarterCosts.slots && (q_iters < h_iters || (q_iters == h_iters && !q_split))) {
         return {4, t_quarters};
       }
-      return {2, t_halves};
+      return {2, choose_tiles_per_split(row_tiles, kHalfCosts, kFineSplitTiles)};
     }
   }
   return {4, choose_tiles_per_split(row_tiles, kQuarterCosts)};

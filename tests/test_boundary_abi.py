@@ -253,7 +253,7 @@ def test_cpu_tensors_have_no_kernel(adapter):
 # KV quarters: 15 / 15 / 0) was fitted until it picks that split for all of
 # them.  The last three run as KV quarters, the rest as halves.
 FASTEST_MEASURED_SPLITS = [
-    ((2357, 512, 2869, 2869), 24),      # config 1: 12 sparse items + 4 tail rows x 3
+    ((2357, 512, 2869, 2869), 28),      # config 1: 12 sparse items + 4 tail rows x 4 (23.5 us; x 3: 24.3)
     ((7680, 512, 8192, 8192), 32),      # config 2, last chunk: 12 + 4 x 5
     ((6272, 2048, 8320, 8320), 72),
     ((16128, 256, 16384, 16384), 32),   # 8 tail rows x 4
@@ -261,7 +261,10 @@ FASTEST_MEASURED_SPLITS = [
     ((8192, 128, 8320, 8320), 32),      # config 3, last chunk: 4 tail rows x 8
     ((15360, 1024, 16384, 16384), 48),
     ((7168, 1024, 8192, 8192), 44),
-    ((3584, 512, 4096, 4096), 28),
+    ((3584, 512, 4096, 4096), 32),      # 25.4 us; 28 items: 26.6
+    ((2048, 512, 2560, 2560), 28),      # 22.2 us; 24 items: 23.0
+    ((3072, 512, 3584, 3584), 32),      # 24.3 us; 28 items: 24.7
+    ((4608, 384, 4992, 4992), 32),      # 26.9 us; 28 items: 27.4
     ((12288, 96, 12384, 12384), 15),
     ((1536, 512, 2048, 2048), 0),       # quarters, no split: 20.6 us against 23.9 as halves
     ((2560, 309, 2869, 2869), 15),      # quarters in one round: 23.3 us against 25.5 as halves
