@@ -15,10 +15,8 @@
  *
  * All pointers are device pointers; `stream` is a hipStream_t (NULL = the
  * null stream).  Every call is asynchronous: it validates its arguments on
- * the host, enqueues the attention kernel on `stream` -- plus one small
- * combine kernel when the chunk has rows long enough to split their keys
- * across workgroups -- and returns.  No call allocates device memory,
- * synchronises, or reads device memory on the host.
+ * the host, enqueues ONE kernel on `stream` and returns.  No call allocates
+ * device memory, synchronises, or reads device memory on the host.
  * Arguments are validated before any HIP call, so a rejected call touches
  * no device state.
  */
@@ -31,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TM_ABI_VERSION 1
+#define TM_ABI_VERSION 2
 
 /* Status codes. */
 #define TM_OK 0
@@ -39,6 +37,13 @@ extern "C" {
 #define TM_ERR_UNSUPPORTED 2      /* outside the fixed compiled geometry or limits */
 #define TM_ERR_WORKSPACE 3        /* workspace too small for this call */
 #define TM_ERR_LAUNCH 4           /* the HIP launch itself failed */
+
+/* A non-empty workspace starts with this many bytes of arrival counters.
+ * They must be zero when a workspace is used for the first time (zero-fill
+ * it once after allocating it); every call that completes leaves them zero,
+ * so one workspace serves any sequence of calls on one stream.  The rest of
+ * the workspace is scratch whose contents do not matter. */
+#define TM_WORKSPACE_COUNTER_BYTES 65536
 
 /* ABI version of the loaded library (TM_ABI_VERSION it was built with). */
 int tm_abi_version(void);
@@ -65,11 +70,13 @@ const char* tm_last_error(void);
  * TilingFunc (operator/op_host/triangle_paged_sparse_attention.cpp:122-237).
  *
  * workspace / workspace_bytes: device scratch of at least
- * tm_triangle_paged_sparse_attention_workspace_size(...) bytes, any content
- * (may be NULL when that size is 0).  It receives the fp32 split-KV partials
- * of row blocks whose keys are split across workgroups (long dense rows);
- * launches that may overlap in time need distinct workspaces.  It must not
- * overlap any input or out.
+ * tm_triangle_paged_sparse_attention_workspace_size(...) bytes (may be NULL
+ * when that size is 0).  Its first TM_WORKSPACE_COUNTER_BYTES hold the
+ * arrival counters of row blocks whose keys are split across workgroups
+ * (long dense rows): zero on first use, left zero by every completed call.
+ * The rest receives their fp32 partials, which the last workgroup of each
+ * such row block merges within the same kernel.  Launches that may overlap
+ * in time need distinct workspaces.  It must not overlap any input or out.
  */
 int tm_triangle_paged_sparse_attention(
     const void* query, const void* key_cache, const void* value_cache,

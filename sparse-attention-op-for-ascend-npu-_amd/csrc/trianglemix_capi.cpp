@@ -90,9 +90,9 @@ constexpr int64_t kHalvesDenseMinTiles = 2048;
 // the greedy dispatch of the items (issued heaviest row block first) onto the
 // slots, an item costing a fixed start-up + merge + store cost plus its tiles,
 // and taking the T with the shortest makespan (ties: larger T, fewer
-// partials); a plan that splits anything also pays for the combine kernel
-// and, per split item, for its fp32 partial (written, then read back by the
-// combine kernel).  Costs are in tile times: a KV-halves workgroup runs a tile
+// partials); a plan that splits anything also pays for the in-launch merge
+// (the last split of a row block reads every partial back) and, per split
+// item, for writing its fp32 partial.  Costs are in tile times: a KV-halves workgroup runs a tile
 // per part and iteration as a quarters one does, but over two parts.  The
 // halves costs are fitted to a forced-T sweep on MI355X: over nine split
 // chunks of 128-2048 rows (prompts 2869-16384) they pick the fastest measured
@@ -109,7 +109,7 @@ constexpr int64_t kHalvesDenseMinTiles = 2048;
 struct PlanCosts {
   int slots;
   int item_fixed_tiles;  // start-up, merge and store of an item
-  int combine_tiles;     // the combine kernel a plan with splits adds
+  int merge_tiles;       // the in-launch merge of a split row block (its last split reads every partial)
   int split_item_tiles;  // each item of a split row block
 };
 constexpr PlanCosts kQuarterCosts{16, 15, 15, 0};  // measured
@@ -138,7 +138,7 @@ int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanC
   }
   int64_t makespan = 0;
   for (int k = 0; k < c.slots; ++k) makespan = slot[k] > makespan ? slot[k] : makespan;
-  return makespan + (split_items > 0 ? c.combine_tiles + c.split_item_tiles * split_items : 0);
+  return makespan + (split_items > 0 ? c.merge_tiles + c.split_item_tiles * split_items : 0);
 }
 
 int choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c, int min_tiles = kMinSplitTiles) {
@@ -195,7 +195,7 @@ ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
       // Quarters keep a split TriangleMix chunk when their plan fits one round
       // of workgroups and its longest item needs fewer loop iterations (4
       // tiles each) than the halves plan's (2 tiles each) -- or as many
-      // without any split, which saves the combine kernel.
+      // without any split, which saves the merge.
       const int t_quarters = choose_tiles_per_split(row_tiles, kQuarterCosts);
       int64_t q_items = 0;
       int q_iters = 0, h_iters = 0;
@@ -246,6 +246,7 @@ struct Geometry {
   int sparse_begin, sparse_end, num_row_blocks, tiles_per_split, kv_parts;
   int64_t items_per_head;
   bool any_split;
+  bool counters_fit;
   int64_t workspace_bytes;
 };
 
@@ -267,7 +268,12 @@ Geometry make_geometry(bool sparse, int64_t query_tokens, int64_t query_start, i
   }
   g.items_per_head = items;
   g.any_split = any_split;
-  g.workspace_bytes = any_split ? int64_t(tmx::kKvHeads) * items * tmx::kPartialBytes : 0;
+  // The counter block holds the arrival counters of at most
+  // kMaxSplitRowBlocks row blocks; a larger chunk whose rows would split
+  // (rows of more than kMaxItemTiles tiles in a chunk of more than 32768
+  // tokens) is refused.
+  g.counters_fit = !any_split || g.num_row_blocks <= tmx::kMaxSplitRowBlocks;
+  g.workspace_bytes = any_split ? tmx::kCounterBytes + int64_t(tmx::kKvHeads) * items * tmx::kPartialBytes : 0;
   return g;
 }
 
@@ -309,6 +315,10 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   }
 
   const Geometry g = make_geometry(sparse, query_tokens, query_start, seq_len, prompt_len);
+  if (!g.counters_fit) {
+    return fail(TM_ERR_UNSUPPORTED, "chunk of %d row blocks splits rows longer than %d keys; the limit is %d row blocks",
+                g.num_row_blocks, tmx::kMaxItemTiles * tmx::kKvTile, tmx::kMaxSplitRowBlocks);
+  }
   if (g.items_per_head > kMaxItemsPerHead) {
     return fail(TM_ERR_UNSUPPORTED, "chunk needs %lld work items per KV head; the limit is %lld",
                 (long long)g.items_per_head, (long long)kMaxItemsPerHead);
@@ -331,7 +341,8 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   p.value_cache = static_cast<const __bf16*>(value_cache);
   p.block_table = block_table;
   p.out = static_cast<__bf16*>(out);
-  p.partials = g.any_split ? static_cast<float*>(workspace) : nullptr;
+  p.counters = g.any_split ? static_cast<unsigned*>(workspace) : nullptr;
+  p.partials = g.any_split ? reinterpret_cast<float*>(static_cast<char*>(workspace) + tmx::kCounterBytes) : nullptr;
   p.num_pages = (int)num_pages;
   p.query_start = (int)query_start;
   p.seq_len = (int)seq_len;
@@ -343,7 +354,7 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   p.any_split = g.any_split ? 1 : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
   const hipError_t err =
-      tmx::launch_triangle_paged_attention(p, sparse, g.any_split, g.kv_parts, static_cast<hipStream_t>(stream));
+      tmx::launch_triangle_paged_attention(p, sparse, g.kv_parts, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) {
     return fail(TM_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   }

@@ -30,6 +30,13 @@ constexpr int kRowBlock = 32;  // query tokens per work item
 // row sum.
 constexpr int64_t kPartialFloats = int64_t(kGroup) * 64 * (64 + 2);
 constexpr int64_t kPartialBytes = kPartialFloats * 4;
+// Workspace of a launch with split row blocks: a block of arrival counters
+// (one per row block, KV head and workgroup position; zero before the launch,
+// and zero again when it completes), then the partials.  The counter block
+// has a fixed size so that it sits at the same place for every geometry: a
+// workspace zeroed once stays valid for any sequence of launches.
+constexpr int64_t kCounterBytes = 65536;
+constexpr int kMaxSplitRowBlocks = int(kCounterBytes / 4 / (kKvHeads * 2));  // 1024
 // Largest number of tiles one work item may hold: the kernel keeps the item's
 // page numbers in two 64-lane registers.  Longer rows are split.
 constexpr int kMaxItemTiles = 128;
@@ -83,6 +90,7 @@ struct KernelParams {
   const int32_t* block_table; // [>= ceil(seq_len/128)]
   __bf16* out;                // [tq, 32, 128]
   float* partials;            // [8][items_per_head] split-KV partials, or null
+  unsigned* counters;         // [8][num_row_blocks][workgroups per item] arrival counters, or null
   int num_pages;
   int query_start;
   int seq_len;
@@ -96,12 +104,11 @@ struct KernelParams {
 };
 
 // Enqueues the attention kernel (TriangleMix mask when `sparse`, plain causal
-// otherwise) and, when some row block is split, the combine kernel that
-// merges its partials (same stream, in order).  kv_parts picks the workgroup
-// shape: 4 (two query heads x KV quarters, items_per_head x 16 workgroups) or
-// 2 (the four heads of the GQA group x KV halves, items_per_head x 8).
-hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, bool any_split, int kv_parts,
-                                           hipStream_t stream);
+// otherwise): one launch, split row blocks included.  kv_parts picks the
+// workgroup shape: 4 (two query heads x KV quarters, items_per_head x 16
+// workgroups) or 2 (the four heads of the GQA group x KV halves,
+// items_per_head x 8).
+hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, int kv_parts, hipStream_t stream);
 
 // Enqueues the paged KV write: token i's K and V rows ([8, 128] bf16, row
 // strides key_stride / value_stride in elements, multiples of 8) go to cache

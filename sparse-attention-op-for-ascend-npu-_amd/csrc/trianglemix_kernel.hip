@@ -17,13 +17,12 @@
 // merge through LDS at the end.  Two waves per SIMD let one wave's softmax
 // run while the other's MFMAs occupy the matrix core.
 // The KV tiles of a row block are cut into splits of at most
-// `tiles_per_split` tiles (host-chosen: at least 1024 keys, at most
+// `tiles_per_split` tiles (host-chosen: at least 768 keys, at most
 // kMaxItemTiles tiles), so only long dense rows split.  A row block with one
 // split writes its output directly; otherwise every split writes an fp32
-// partial (O, row max, row sum) to the workspace and a small combine kernel,
-// enqueued right after on the same stream, merges the partials in split order
-// (deterministic) and writes the output.  Chunks without long rows -- every
-// sparse middle chunk -- are one launch.
+// partial (O, row max, row sum) to the workspace and counts its arrival, and
+// the workgroup that arrives last merges all partials in split order
+// (deterministic) and writes the output -- every chunk is one launch.
 // Items are numbered per KV head, heaviest row blocks first; KV head =
 // blockIdx % 8 keeps every workgroup of one KV head on one XCD (workgroups
 // are dispatched round-robin over the 8 XCDs), so both head pairs of a row
@@ -100,6 +99,7 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 #define TM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
@@ -274,6 +274,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   __shared__ __attribute__((aligned(1024))) char v_lds1[S::kSlotBytes];
   // Q of the workgroup's heads: [head][row][16-byte slot], K's swizzle.
   __shared__ __attribute__((aligned(1024))) char q_lds[H * kRowBlock * kRowBytes];
+  __shared__ int s_last;  // this workgroup completed its row block's splits
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, kept scalar
@@ -710,8 +711,10 @@ triangle_paged_attention_kernel(KernelParams p) {
     m_run = mt;
   }
 
-  if (nsplit == 1) {
-    const float l_tot = half_sum(l_run);  // the two 32-lane halves hold one row
+  // Normalise the O merged d-blocks (row sum: the two 32-lane halves hold
+  // one row) and store them as bf16, rounded to nearest even.
+  auto store_rows = [&](const f32x16_t* blocks, float l_lane) {
+    const float l_tot = half_sum(l_lane);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (!row_active) return;
     __bf16* orow = p.out + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim;
@@ -721,158 +724,134 @@ triangle_paged_attention_kernel(KernelParams p) {
       for (int g = 0; g < 4; ++g) {
         bf16x4_t o4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(kept[o][4 * g + e] * inv);
+        for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(blocks[o][4 * g + e] * inv);
         *reinterpret_cast<bf16x4_t*>(orow + 32 * (kq * O + o) + 8 * g + 4 * half) = o4;
       }
     }
+  };
+  if (nsplit == 1) {
+    store_rows(kept, l_run);
     return;
   }
 
-  // ---- split-KV: publish this split's partial; the combine kernel merges ----
-  // Layout per (KV head, item): O [hq][m][v/4][lane][v%4], then row max
-  // [hq][lane], then the lane's partial row sum [hq][lane] -- every access is
-  // a lane-contiguous 16- or 4-byte vector.  Workgroups of one item write
-  // disjoint heads, the parts disjoint d-blocks.
-  float* part = p.partials + ((size_t)kvh * p.items_per_head + item) * kPartialFloats;
+  // ---- split-KV, merged in this launch ----
+  // Every split publishes its partial; the workgroup whose arrival completes
+  // the row block (per workgroup position hp) merges all partials in split
+  // order -- the same sums whichever split arrives last, so the result is
+  // deterministic -- and writes the output.  Record per (KV head, item):
+  // O [hq][d-block][v/4][lane][v%4] (unnormalised), then row max [hq][lane] and the
+  // lane's partial row sum [hq][lane]; workgroups of one item write disjoint
+  // heads, the parts disjoint d-blocks.  The records are written and read
+  // with the sc1 cache policy (agent scope: stores written through to the
+  // level where every L2 of the GPU is coherent, loads served from it), and
+  // the arrival counter is an agent-scope atomic, so no fence (a whole-L2
+  // writeback and invalidate) is needed.  Each wave waits for its own stores
+  // before the workgroup's arrival is counted; the workgroup that counts last
+  // has seen every other split arrive after their stores completed.
+  constexpr int kCpolAgent = 16;               // sc1
+  constexpr int kStatM = kGroup * 64 * 64;     // row maxima [hq][lane]
+  constexpr int kStatL = kGroup * 64 * 65;     // partial row sums [hq][lane]
+  const int first = item - split;
+  // Buffer over the row block's records (offsets stay 32-bit for any chunk).
+  const __amdgpu_buffer_rsrc_t rec = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.partials + ((size_t)kvh * p.items_per_head + first) * kPartialFloats), (short)0,
+      nsplit * (int)kPartialBytes, kBufferFlags);
+  // 16-byte piece g of d-block o: each instruction moves 64 lanes x 16 B = 1 KB contiguous.
+  auto blk_off = [&](int s, int o, int g) {
+    return (unsigned)(s * (int)kPartialBytes + ((((hq * 4 + kq * O + o) * 4 + g) * 64 + lane) * 4) * 4);
+  };
+  {
 #pragma unroll
-  for (int o = 0; o < O; ++o) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4_t o4 = {kept[o][4 * g], kept[o][4 * g + 1], kept[o][4 * g + 2], kept[o][4 * g + 3]};
-      *reinterpret_cast<f32x4_t*>(part + (((hq * 4 + kq * O + o) * 4 + g) * 64 + lane) * 4) = o4;
-    }
-  }
-  if (kq == 0) {  // every part holds the same merged row max and row sum
-    part[kGroup * 64 * 64 + hq * 64 + lane] = m_run;
-    part[kGroup * 64 * 65 + hq * 64 + lane] = l_run;
-  }
-}
-
-// Merge the split-KV partials of every split row block with the online-
-// softmax rescale rule, then normalise and write bf16.  One workgroup per
-// (row block, KV head, query head of the group) with one wave per 32-wide
-// d-block; unsplit row blocks exit.  Each wave reads the row maxima and row
-// sums of all splits first, then the O partials eight splits at a time, so
-// the loads of a batch are independent of each other and stay in flight
-// together; the weighted sums run in split order (deterministic).
-constexpr int kCombineThreads = (kHeadDim / 32) * 64;
-constexpr int kCombineBatch = 8;
-
-template <bool kSparse>
-__global__ void __launch_bounds__(kCombineThreads)
-triangle_paged_attention_combine_kernel(KernelParams p) {
-  const int tid = threadIdx.x;
-  const int m = tid >> 6;  // d-block
-  const int lane = tid & 63;
-  const int n = lane & 31;
-  const int half = lane >> 5;
-  const int kvh = blockIdx.x % kKvHeads;
-  const int hq = (blockIdx.x / kKvHeads) % kGroup;
-  const int order = blockIdx.x / (kKvHeads * kGroup);
-  const int sparse_begin = kSparse ? p.sparse_begin : 0;
-  const int sparse_end = kSparse ? p.sparse_end : 0;
-
-  // First item of this row block = sum of the split counts of the row blocks
-  // issued before it (wave-wide prefix sum, as in decode_item).
-  int first_item = 0, nsplit = 1;
-  for (int base = 0; base <= order; base += 64) {
-    const int o = base + lane;
-    const int cnt = o <= order ? row_block_splits(o, p.num_row_blocks, p.query_start, p.seq_len, sparse_begin,
-                                                  sparse_end, p.tiles_per_split)
-                               : 0;
-    int incl = cnt;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int t = __shfl_up(incl, d);
-      if (lane >= d) incl += t;
-    }
-    if (order < base + 64) {
-      const int src = order - base;
-      nsplit = __shfl(cnt, src);
-      first_item += __shfl(incl - cnt, src);
-    } else {
-      first_item += __shfl(incl, 63);
-    }
-  }
-  first_item = __builtin_amdgcn_readfirstlane(first_item);
-  nsplit = __builtin_amdgcn_readfirstlane(nsplit);
-  if (nsplit == 1) return;
-
-  const int rb = p.num_row_blocks - 1 - order;
-  const int q = p.query_start + rb * kRowBlock + n;
-  const bool row_active = q < p.seq_len;
-  const int head = kvh * kGroup + hq;
-  const float* base = p.partials + ((size_t)kvh * p.items_per_head + first_item) * kPartialFloats;
-  const int m_off = kGroup * 64 * 64 + hq * 64 + lane;  // row max of this lane's row
-  const int l_off = kGroup * 64 * 65 + hq * 64 + lane;  // this lane's partial row sum
-
-  // One pass over the splits, eight at a time: the running max mt rescales
-  // what is already summed when a batch raises it (the online-softmax rule),
-  // so the row maxima need no round trip of their own.  Splits are summed in
-  // order (deterministic).
-  float mt = -INFINITY;
-  float lt = 0.0f;
-  f32x4_t ot[4] = {};  // [v/4] of d-block m, 4 consecutive v each
-  for (int s0 = 0; s0 < nsplit; s0 += kCombineBatch) {
-    f32x4_t os[kCombineBatch][4];
-    float w[kCombineBatch], ls[kCombineBatch];
-#pragma unroll
-    for (int b = 0; b < kCombineBatch; ++b) {
-      const int s = min(s0 + b, nsplit - 1);  // past the last split: a repeated load, weighted 0 below
-      const float* part = base + (size_t)s * kPartialFloats;
+    for (int o = 0; o < O; ++o) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        os[b][g] = *reinterpret_cast<const f32x4_t*>(part + (((hq * 4 + m) * 4 + g) * 64 + lane) * 4);
+        const f32x4_t x = {kept[o][4 * g], kept[o][4 * g + 1], kept[o][4 * g + 2], kept[o][4 * g + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, x), rec, blk_off(split, o, g), 0,
+                                               kCpolAgent);
       }
-      w[b] = part[m_off];
-      ls[b] = part[l_off];
+    }
+    if (kq == 0) {  // every part holds the same merged row max and row sum
+      const unsigned so = (unsigned)(split * (int)kPartialBytes + (hq * 64 + lane) * 4);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run), rec, so + kStatM * 4, 0, kCpolAgent);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), rec, so + kStatL * 4, 0, kCpolAgent);
+    }
+  }
+  wait_dma();  // this wave's partial stores completed (vmcnt also counts stores)
+  __syncthreads();
+  unsigned* ctr = p.counters + ((size_t)kvh * p.num_row_blocks + rb) * S::kWgPerKvHead + hp;
+  if (tid == 0) {
+    s_last = (int)(__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (unsigned)(nsplit - 1));
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // Leave the counter zero for the next launch (every split has arrived).
+  if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // One pass over the splits, kMergeBatch at a time with all of a batch's
+  // loads in flight: a batch that raises the running max rescales what is
+  // already summed (the online-softmax rule).  Splits past the last are
+  // loaded again and weighted 0.
+  constexpr int kMergeBatch = 4;
+  f32x16_t acc[kHeadDim / 32 / 2];
+#pragma unroll
+  for (int o = 0; o < O; ++o) acc[o] = f32x16_t{};
+  float mt = -INFINITY, lt = 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
+    float ms[kMergeBatch], ls[kMergeBatch];
+    f32x4_t xs[kMergeBatch][kHeadDim / 32 / 2][4];
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) {
+      const int sb = min(s0 + b, nsplit - 1);
+      const unsigned so = (unsigned)(sb * (int)kPartialBytes + (hq * 64 + lane) * 4);
+      ms[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rec, so + kStatM * 4, 0, kCpolAgent));
+      ls[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rec, so + kStatL * 4, 0, kCpolAgent));
+#pragma unroll
+      for (int o = 0; o < O; ++o) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          xs[b][o][g] =
+              __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rec, blk_off(sb, o, g), 0, kCpolAgent));
+        }
+      }
     }
     float mb = mt;
 #pragma unroll
-    for (int b = 0; b < kCombineBatch; ++b) mb = s0 + b < nsplit ? fmaxf(mb, w[b]) : mb;
-    const float mu = mb == -INFINITY ? 0.0f : mb;  // all maxima so far -inf: nothing is summed yet
+    for (int b = 0; b < kMergeBatch; ++b) mb = s0 + b < nsplit ? fmaxf(mb, ms[b]) : mb;
+    const float mu = mb == -INFINITY ? 0.0f : mb;  // no keys in any split so far: nothing summed yet
     const float keep = mt == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mt - mu);
     lt *= keep;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) ot[g] *= keep;
+    for (int o = 0; o < O; ++o) acc[o] *= keep;
 #pragma unroll
-    for (int b = 0; b < kCombineBatch; ++b) {
-      const float wb = s0 + b < nsplit ? __builtin_amdgcn_exp2f(w[b] - mu) : 0.0f;
-      lt += ls[b] * wb;
+    for (int b = 0; b < kMergeBatch; ++b) {
+      const float w = s0 + b < nsplit ? __builtin_amdgcn_exp2f(ms[b] - mu) : 0.0f;
+      lt += ls[b] * w;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) ot[g] += os[b][g] * wb;
+      for (int o = 0; o < O; ++o) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[o][4 * g + e] += xs[b][o][g][e] * w;
+        }
+      }
     }
     mt = mb;
   }
-  const float l_tot = half_sum(lt);  // the two 32-lane halves hold one row
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (!row_active) return;
-  __bf16* orow = p.out + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    bf16x4_t o4;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(ot[g][e] * inv);
-    *reinterpret_cast<bf16x4_t*>(orow + 32 * m + 8 * g + 4 * half) = o4;
-  }
+  store_rows(acc, lt);
 }
 
 template <bool kSparse, int P>
-hipError_t launch(const KernelParams& p, bool any_split, hipStream_t stream) {
+hipError_t launch(const KernelParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((triangle_paged_attention_kernel<kSparse, P>),
                      dim3((unsigned)(p.items_per_head * Shape<P>::kWgPerKvHead * kKvHeads)), dim3(kThreads), 0,
                      stream, p);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || !any_split) return err;
-  hipLaunchKernelGGL(triangle_paged_attention_combine_kernel<kSparse>,
-                     dim3((unsigned)(p.num_row_blocks * kKvHeads * kGroup)), dim3(kCombineThreads), 0, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, bool any_split, int kv_parts,
-                                           hipStream_t stream) {
-  if (kv_parts == 2) return sparse ? launch<true, 2>(p, any_split, stream) : launch<false, 2>(p, any_split, stream);
-  return sparse ? launch<true, 4>(p, any_split, stream) : launch<false, 4>(p, any_split, stream);
+hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, int kv_parts, hipStream_t stream) {
+  if (kv_parts == 2) return sparse ? launch<true, 2>(p, stream) : launch<false, 2>(p, stream);
+  return sparse ? launch<true, 4>(p, stream) : launch<false, 4>(p, stream);
 }
 
 }  // namespace tmx

@@ -26,15 +26,24 @@
 // the same predicates and messages ("GPU" for "NPU").  Launches go on the
 // current HIP stream of the query's device under a device guard, with no
 // host synchronisation.  When the library reports a non-zero split-KV
-// workspace it is taken from PyTorch's caching allocator for the call, as the
-// reference's EXEC_NPU_CMD takes the aclnn workspace from torch_npu's
-// allocator (stream-ordered reuse keeps it valid until the kernels finish).
+// workspace, it comes from a buffer kept per (device, stream) -- allocated
+// from PyTorch's caching allocator, as the reference's EXEC_NPU_CMD takes the
+// aclnn workspace from torch_npu's -- whose arrival counters are zeroed once
+// when it is created (the kernel leaves them zero).  Launches on one stream
+// run in order, so they share it; under stream capture each call gets a
+// buffer of its own from the capture's memory, with the counters cleared by a
+// captured fill.
 
 #include <ATen/ATen.h>
 #include <ATen/MemoryOverlap.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime.h>
 #include <torch/library.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/trianglemix.h"
 
@@ -79,6 +88,31 @@ void check_output(const at::Tensor& query, const at::Tensor& key_cache, const at
   at::assert_no_overlap(output, block_table);
 }
 
+// Split-KV workspace for a launch on `stream` (see the file comment).
+at::Tensor workspace_for(const at::Tensor& like, int64_t bytes, void* stream) {
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  TORCH_CHECK(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &capture) == hipSuccess,
+              "hipStreamIsCapturing failed");
+  const auto options = like.options().dtype(at::kByte);
+  if (capture != hipStreamCaptureStatusNone) {
+    at::Tensor ws = at::empty({bytes}, options);
+    ws.narrow(0, 0, TM_WORKSPACE_COUNTER_BYTES).zero_();
+    return ws;
+  }
+  static std::mutex mutex;
+  static std::map<std::pair<int, void*>, at::Tensor> cache;
+  std::lock_guard<std::mutex> lock(mutex);
+  at::Tensor& ws = cache[{like.device().index(), stream}];
+  if (!ws.defined() || ws.numel() < bytes) {
+    // Grow geometrically; the old buffer is released to the caching
+    // allocator, which reuses it only after the work queued on this stream.
+    const int64_t size = ws.defined() ? std::max(bytes, 2 * ws.numel()) : bytes;
+    ws = at::empty({size}, options);
+    ws.narrow(0, 0, TM_WORKSPACE_COUNTER_BYTES).zero_();
+  }
+  return ws;
+}
+
 void check_status(int status, const char* what) {
   TORCH_CHECK(status == TM_OK, what, " failed (", tm_status_string(status), "): ", tm_last_error());
 }
@@ -94,7 +128,7 @@ void run(const at::Tensor& query, const at::Tensor& key_cache, const at::Tensor&
   TORCH_CHECK(ws >= 0, "invalid attention attributes: ", tm_last_error());
   void* stream = c10::hip::getCurrentHIPStream(query.device().index()).stream();
   at::Tensor ws_tensor;
-  if (ws > 0) ws_tensor = at::empty({ws}, query.options().dtype(at::kByte));
+  if (ws > 0) ws_tensor = workspace_for(query, ws, stream);
   void* workspace = ws > 0 ? ws_tensor.data_ptr() : nullptr;
   const int status =
       sparse ? tm_triangle_paged_sparse_attention(

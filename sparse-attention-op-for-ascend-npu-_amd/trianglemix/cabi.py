@@ -48,6 +48,14 @@ def workspace_size(query_tokens: int, query_start: int, seq_len: int, prompt_len
     return int(n)
 
 
+# Split-KV workspace per (device, stream): the first WORKSPACE_COUNTER_BYTES
+# are arrival counters that must be zero before a workspace's first use (the
+# kernel leaves them zero), so a buffer is zero-filled once when created and
+# then kept -- alive for as long as work queued on its stream may use it.
+WORKSPACE_COUNTER_BYTES = 65536
+_WORKSPACES: dict = {}
+
+
 def _workspace(query, query_start, seq_len, prompt_len, workspace, stream):
     need = workspace_size(query.shape[0], query_start, seq_len, prompt_len)
     if need == 0:
@@ -55,7 +63,13 @@ def _workspace(query, query_start, seq_len, prompt_len, workspace, stream):
     if workspace is None:
         import torch
 
-        workspace = torch.empty(need, dtype=torch.uint8, device=query.device)
+        key = (query.device.index, int(stream))
+        workspace = _WORKSPACES.get(key)
+        if workspace is None or workspace.numel() < need:
+            size = need if workspace is None else max(need, 2 * workspace.numel())
+            with torch.cuda.stream(torch.cuda.ExternalStream(int(stream), device=query.device)):
+                workspace = torch.zeros(size, dtype=torch.uint8, device=query.device)
+            _WORKSPACES[key] = workspace
     return workspace.data_ptr(), workspace.numel() * workspace.element_size()
 
 
