@@ -97,6 +97,28 @@ int64_t tm_triangle_paged_sparse_attention_workspace_size(
     int64_t prompt_len);
 
 /*
+ * The same TriangleMix call for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * has no counterpart in the reference.  No call allocates: the split-KV
+ * scratch (arrival counters + partials) is a static array of 32 MiB per GPU,
+ * held until the process ends; a chunk that needs more is refused with
+ * TM_ERR_WORKSPACE before any HIP call.  The device address of the array is
+ * looked up once per device, with that device current -- call with the
+ * stream's device current, as for any launch.  All calls in one process on
+ * one GPU share the array: calls that may overlap in time on that GPU (on
+ * different streams, or graphs replayed on different streams) race and must
+ * not be made.  The counters start zero and each completed call leaves them
+ * zero.  Other arguments, results and errors as
+ * tm_triangle_paged_sparse_attention.
+ */
+int tm_triangle_paged_sparse_attention_noalloc(
+    const void* query, const void* key_cache, const void* value_cache,
+    const int32_t* block_table, void* out,
+    int64_t query_tokens, int64_t num_pages, int64_t block_table_cols,
+    int64_t query_start, int64_t seq_len, int64_t prompt_len, float scale,
+    void* stream);
+
+/*
  * Dense paged causal prefill (row q attends [0, q]) built from the same
  * tiles; serves unselected layers and fallbacks.  Replaces the dense CANN
  * FIA call the reference falls back to

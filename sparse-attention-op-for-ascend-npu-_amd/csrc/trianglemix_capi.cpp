@@ -396,6 +396,30 @@ int64_t tm_triangle_paged_sparse_attention_workspace_size(int64_t query_tokens, 
   return make_geometry(true, query_tokens, query_start, seq_len, prompt_len).workspace_bytes;
 }
 
+int tm_triangle_paged_sparse_attention_noalloc(const void* query, const void* key_cache, const void* value_cache,
+                                               const int32_t* block_table, void* out, int64_t query_tokens,
+                                               int64_t num_pages, int64_t block_table_cols, int64_t query_start,
+                                               int64_t seq_len, int64_t prompt_len, float scale, void* stream) {
+  g_last_error[0] = '\0';
+  // Attributes first (same errors as the workspace entry point), then the
+  // scratch this geometry needs against what the per-GPU array holds.
+  const int st = check_attributes(query_tokens, query_start, seq_len, prompt_len, true);
+  if (st != TM_OK) return st;
+  const int64_t need = make_geometry(true, query_tokens, query_start, seq_len, prompt_len).workspace_bytes;
+  if (need > tmx::kNoAllocScratchBytes) {
+    return fail(TM_ERR_WORKSPACE,
+                "chunk needs %lld bytes of split-KV scratch; the no-allocation entry point holds %lld per GPU",
+                (long long)need, (long long)tmx::kNoAllocScratchBytes);
+  }
+  void* scratch = nullptr;
+  if (need > 0) {
+    const hipError_t err = tmx::noalloc_scratch(&scratch);
+    if (err != hipSuccess) return fail(TM_ERR_LAUNCH, "no-allocation scratch lookup failed: %s", hipGetErrorString(err));
+  }
+  return launch(true, query, key_cache, value_cache, block_table, out, query_tokens, num_pages, block_table_cols,
+                query_start, seq_len, prompt_len, scale, scratch, need > 0 ? tmx::kNoAllocScratchBytes : 0, stream);
+}
+
 int tm_dense_paged_causal_attention(const void* query, const void* key_cache, const void* value_cache,
                                     const int32_t* block_table, void* out, int64_t query_tokens,
                                     int64_t num_pages, int64_t block_table_cols, int64_t query_start,

@@ -37,6 +37,10 @@ constexpr int64_t kPartialBytes = kPartialFloats * 4;
 // workspace zeroed once stays valid for any sequence of launches.
 constexpr int64_t kCounterBytes = 65536;
 constexpr int kMaxSplitRowBlocks = int(kCounterBytes / 4 / (kKvHeads * 2));  // 1024
+// Split-KV scratch held per GPU for the no-allocation entry point (counter
+// block + partials): enough for the TriangleMix chunks of up to 2048 rows
+// at L <= 16384 that split their dense-tail rows.
+constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
 // Largest number of tiles one work item may hold: the kernel keeps the item's
 // page numbers in two 64-lane registers.  Longer rows are split.
 constexpr int kMaxItemTiles = 128;
@@ -109,6 +113,10 @@ struct KernelParams {
 // workgroups) or 2 (the four heads of the GQA group x KV halves,
 // items_per_head x 8).
 hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, int kv_parts, hipStream_t stream);
+
+// Device address of this GPU's no-allocation scratch (kNoAllocScratchBytes,
+// 256-byte aligned), looked up once per device with the device current.
+hipError_t noalloc_scratch(void** ptr);
 
 // Enqueues the paged KV write: token i's K and V rows ([8, 128] bf16, row
 // strides key_stride / value_stride in elements, multiples of 8) go to cache

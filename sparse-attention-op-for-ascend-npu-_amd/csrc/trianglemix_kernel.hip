@@ -90,6 +90,8 @@
 
 #include <stdint.h>
 
+#include <mutex>
+
 #include "trianglemix_kernel.h"
 
 namespace tmx {
@@ -852,6 +854,32 @@ hipError_t launch(const KernelParams& p, hipStream_t stream) {
 hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, int kv_parts, hipStream_t stream) {
   if (kv_parts == 2) return sparse ? launch<true, 2>(p, stream) : launch<false, 2>(p, stream);
   return sparse ? launch<true, 4>(p, stream) : launch<false, 4>(p, stream);
+}
+
+// Split-KV scratch of the no-allocation entry point: one array per GPU for
+// the life of the process.  Zero at load; every completed launch leaves its
+// arrival counters zero again.  In host code `scratch` is only a stand-in
+// for the symbol: its device address comes from hipGetSymbolAddress, once
+// per device, and only that address is ever handed to a kernel.
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+hipError_t noalloc_scratch(void** ptr) {
+  constexpr int kMaxDevices = 64;
+  static void* addresses[kMaxDevices] = {};
+  static std::mutex mutex;
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return err;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mutex);
+  if (addresses[device] == nullptr) {
+    void* address = nullptr;
+    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));  // with `device` current
+    if (err != hipSuccess) return err;
+    addresses[device] = address;
+  }
+  *ptr = addresses[device];
+  return hipSuccess;
 }
 
 }  // namespace tmx

@@ -85,6 +85,17 @@ def triangle_paged_sparse_attention(query, key_cache, value_cache, block_table, 
         float(scale), ws_ptr, ws_bytes, st))
 
 
+def triangle_paged_sparse_attention_noalloc(query, key_cache, value_cache, block_table, out, *, query_start: int,
+                                            seq_len: int, prompt_len: int, scale: float, stream=None) -> None:
+    """The no-allocation entry point: split-KV scratch from the library's static per-GPU array."""
+    lib = load_hip_library()
+    st = _stream(query, stream)
+    _check(lib.tm_triangle_paged_sparse_attention_noalloc(
+        query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(), out.data_ptr(),
+        query.shape[0], key_cache.shape[0], block_table.shape[-1], query_start, seq_len, prompt_len,
+        float(scale), st))
+
+
 def dense_paged_causal_attention(query, key_cache, value_cache, block_table, out, *, query_start: int,
                                  seq_len: int, scale: float, stream=None, workspace=None) -> None:
     lib = load_hip_library()

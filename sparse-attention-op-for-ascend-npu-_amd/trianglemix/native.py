@@ -69,6 +69,9 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.tm_triangle_paged_sparse_attention.restype = ctypes.c_int
     lib.tm_triangle_paged_sparse_attention.argtypes = [
         vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ctypes.c_float, vp, i64, vp]
+    lib.tm_triangle_paged_sparse_attention_noalloc.restype = ctypes.c_int
+    lib.tm_triangle_paged_sparse_attention_noalloc.argtypes = [
+        vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, ctypes.c_float, vp]
     lib.tm_triangle_paged_sparse_attention_workspace_size.restype = i64
     lib.tm_triangle_paged_sparse_attention_workspace_size.argtypes = [i64, i64, i64, i64]
     lib.tm_dense_paged_causal_attention.restype = ctypes.c_int

@@ -65,6 +65,7 @@ def test_header_functions_are_exported(lib):
     assert names == sorted([
         "tm_abi_version", "tm_status_string", "tm_last_error",
         "tm_triangle_paged_sparse_attention", "tm_triangle_paged_sparse_attention_workspace_size",
+        "tm_triangle_paged_sparse_attention_noalloc",
         "tm_dense_paged_causal_attention", "tm_dense_paged_causal_attention_workspace_size",
         "tm_reshape_and_cache"])
     raw = ctypes.CDLL(str(native.HIP_LIBRARY))
@@ -166,6 +167,19 @@ def test_kv_write_validation_errors(lib, over, status, msg):
 def test_kv_write_without_tokens_enqueues_nothing(lib):
     # no pointer is dereferenced and no HIP call is made for an empty chunk
     assert _kv_write(lib, tokens=0, key=None, value=None, slots=None) == 0
+
+
+def test_noalloc_refuses_chunks_beyond_its_scratch_without_hip_calls(lib):
+    # fake (never dereferenced) pointers: both refusals happen before any HIP call
+    fake = ctypes.c_void_p(0x1000)
+    # invalid attributes: the same error as the workspace entry point
+    r = lib.tm_triangle_paged_sparse_attention_noalloc(fake, fake, fake, fake, fake, 512, 64, 64, 4096, 4000, 8192,
+                                                       0.088, None)
+    assert r == 1 and "Tq == seq_len" in lib.tm_last_error().decode()
+    # a dense 2048-row tail at L = 131072 needs ~100 MB of split scratch: more than the 32 MiB array
+    r = lib.tm_triangle_paged_sparse_attention_noalloc(fake, fake, fake, fake, fake, 2048, 1024, 1024, 129024,
+                                                       131072, 131072, 0.088, None)
+    assert r == 3 and "no-allocation" in lib.tm_last_error().decode()
 
 
 def test_workspace_sizes(lib):
