@@ -1,0 +1,113 @@
+"""Long-context correctness: BASELINE config 4 (L = 32768 and 131072, chunk 2048).
+
+At L = 131072 a dense-tail row attends 131072 keys = 4096 tiles, which the
+planner splits into many work items merged inside the launch; the position,
+row-index and page arithmetic run at sizes no other test reaches.  The
+reference pins its longest case the same way (operator/tests/npu_v2_correctness.py:53-216,
+``long_random_paged_8192``) and keeps an exact on-device reference
+(operator/op_kernel/triangle_paged_sparse_attention.cpp:22-322).
+
+* Oracle parity (N(0,1) bf16, random page table) on row subsets of the
+  prompt's last chunk -- its first rows, the rows around ``prompt - 128``
+  where sparse rows end, and the deepest dense-tail rows -- and of a middle
+  chunk; tolerances as everywhere (max-abs 2e-2, mean-abs 2e-3, rel-L2 2e-2).
+* The exact mask identity over the WHOLE last chunk: Q = 0 weighs every
+  attended key 1/|S|, and one-hot residue V rows turn each output row into
+  the residue histogram of its key set (8 moduli), so one added, dropped or
+  shifted key of any row changes the output.  Counts and sums are exact
+  integers in fp32; bf16 rounding of count/|S| (half an ulp) is the only
+  difference allowed.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import geometry as OG
+from trianglemix import cabi
+from trianglemix.workload import SCALE, make_cache, make_query
+
+pytestmark = pytest.mark.gpu
+
+CHUNK = 2048
+MAX_ABS, MEAN_ABS, REL_L2 = 2e-2, 2e-3, 2e-2
+
+
+def _sparse(gpu, q, kd, vd, btd, qs, seq, prompt):
+    qd = q.to(gpu)
+    out = torch.full_like(qd, float("nan"))
+    cabi.triangle_paged_sparse_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, prompt_len=prompt,
+                                         scale=SCALE)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("L", [32768, 131072])
+def test_long_context_rows_match_oracle(gpu, L):
+    prompt = L
+    k, v, bt = make_cache(L, 700 + L // 1024, std=1.0)
+    kd, vd, btd = k.to(gpu), v.to(gpu), bt.to(gpu)
+    cases = [  # (label, query_start, rows of the chunk checked against the oracle)
+        ("last", L - CHUNK, [(0, 32), (CHUNK - 136, CHUNK - 120), (CHUNK - 8, CHUNK)]),
+        ("middle", L // 2, [(0, 16), (1000, 1032), (CHUNK - 16, CHUNK)]),
+    ]
+    for label, qs, windows in cases:
+        seq = qs + CHUNK
+        q = make_query(CHUNK, 900 + qs // 1024, std=1.0)
+        need = cabi.workspace_size(CHUNK, qs, seq, prompt)
+        print(f"L={L} {label} chunk qs={qs} workspace={need}", flush=True)
+        got = _sparse(gpu, q, kd, vd, btd, qs, seq, prompt)
+        assert torch.isfinite(got.float()).all(), (L, label)
+        for r0, r1 in windows:
+            expected = OA.attention_torch(q[r0:r1], k, v, bt, qs + r0, seq, prompt, SCALE)
+            m = OA.error_metrics(got[r0:r1].float().numpy(), expected.float().numpy())
+            print(f"L={L} {label} rows {qs + r0}..{qs + r1 - 1}: {m}", flush=True)
+            assert m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS and m["relative_l2"] <= REL_L2, (L, label,
+                                                                                                         r0, m)
+    assert cabi.workspace_size(CHUNK, L - CHUNK, L, prompt) > cabi.WORKSPACE_COUNTER_BYTES  # dense tail split
+
+
+def _residue_histogram(intervals, m):
+    """Count of keys k in the union of ``intervals`` with k % m == d, for d in 0..127."""
+    d = np.arange(128)
+    hist = np.zeros(128, dtype=np.int64)
+    for b, e in intervals:
+        # keys k in [b, e) with k = d (mod m): floor((e-1-d)/m) - floor((b-1-d)/m)
+        hist += (e - 1 - d) // m - (b - 1 - d) // m
+    hist[d >= m] = 0
+    return hist
+
+
+@pytest.mark.parametrize("L", [32768, 131072])
+def test_long_context_mask_identity_whole_last_chunk(gpu, L):
+    qs, seq, prompt = L - CHUNK, L, L
+    _, _, bt = make_cache(L, 800 + L // 1024)
+    pages = int(bt.max()) + 1
+    moduli = [128, 127, 125, 123, 121, 119, 113, 109]
+    table = bt[0].tolist()
+    tok = torch.arange(seq)
+    v = torch.zeros(pages, 128, 8, 128, dtype=torch.bfloat16)
+    for h, m in enumerate(moduli):
+        onehot = torch.nn.functional.one_hot(tok % m, 128).to(torch.bfloat16).reshape(-1, 128, 128)
+        full = seq // 128
+        v[torch.tensor(table[:full]), :, h] = onehot[:full]
+        if seq % 128:
+            v[table[full], :seq % 128, h] = onehot.reshape(-1, 128)[full * 128:seq]
+    k = torch.zeros_like(v)
+    q = torch.zeros(CHUNK, 32, 128, dtype=torch.bfloat16)
+    actual = _sparse(gpu, q, k.to(gpu), v.to(gpu), bt.to(gpu), qs, seq, prompt).float().numpy()
+    expected = np.zeros((CHUNK, 32, 128))
+    for r in range(CHUNK):
+        ivs = OG.selected_intervals(qs + r, seq, prompt)
+        n = sum(e - b for b, e in ivs)
+        for h, m in enumerate(moduli):
+            expected[r, 4 * h:4 * h + 4] = _residue_histogram(ivs, m) / n
+    # the histograms' own check: every row's counts add up to |S|
+    assert all(_residue_histogram(OG.selected_intervals(qs + r, seq, prompt), 128).sum() ==
+               sum(e - b for b, e in OG.selected_intervals(qs + r, seq, prompt)) for r in (0, CHUNK - 1))
+    tol = np.maximum(np.abs(expected) * 2.0 ** -8, 1e-30)
+    bad = np.abs(actual - expected) > tol
+    assert not bad.any(), f"{bad.sum()} mismatching entries, first at {np.argwhere(bad)[0]}"
