@@ -4,41 +4,43 @@ Workload (the headline configuration): Qwen3-8B attention geometry (Hq=32, Hkv=8
 D=128, bf16, page 128), one request, prompt L=8192 prefilled in 16 chunks of
 512.  One *step* = the 16 chunk launches of the sparse kernel, in order, over
 one paged K/V cache (random block-table permutation) that already holds the
-whole prompt's K/V; all inputs are resident in HBM before timing.
+whole prompt's K/V; all inputs are resident in HBM before timing.  Every
+chunk is one kernel launch.
 
 Reported JSON line (rank 0 only):
 
-* ``value`` -- mean microseconds per chunk of the sparse kernel (graph
-  replay of the 16 launches, HIP events on the launch stream);
+* ``value`` -- mean microseconds per chunk of the sparse kernel over the K
+  timed steps (HIP-graph replay of the 16 launches, HIP events on the launch
+  stream); the K steps run in windows that alternate with the dense
+  companion's in ABBA order, and ``timing`` gives the windows' median,
+  inter-quartile range, p10 and Tukey-fence outliers beside the mean;
 * ``roofline`` -- bf16 MFMA bound: algorithmic FLOPs per launch
   (4*D*Hq*attended pairs) / average launch duration, vs 2.5 PFLOP/s;
   ``traffic`` is the rocprofv3 FETCH+WRITE bytes per launch when a summary
   for this workload exists under profiles/, else null;
 * ``dense`` -- the same 16 chunks through the dense paged causal companion
-  kernel, and the attention-time cut of sparse vs dense (ABBA order);
+  kernel, and the attention-time cut of sparse vs dense;
 * ``kv_write`` -- the paged KV write upstream of the attention
   (``trianglemix::reshape_and_cache``): one chunk's fresh K/V into its pages,
-  and the whole prompt in one call, with HBM GB/s against 8 TB/s (it moves
-  each token's 2 KB K row and 2 KB V row in and out);
+  and the whole prompt in one call, with HBM GB/s against 8 TB/s;
 * ``cpu_baseline`` -- the fp32 PyTorch CPU masked-attention restatement of the
   reference's oracle (``oracle.attention.attention_torch``) over all 16
-  chunks, median of 2 passes after a warm-up, on this host's cores.
+  chunks on this host's cores (``torch.set_num_threads(os.cpu_count())``):
+  one warm-up pass, then the median of 3 passes;
+* ``legs`` -- the other BASELINE configurations, measured in the same run:
+  config 1 (one launch: rows 2357..2868 of a 2869-token prompt), config 3
+  (L=8320 in chunks of 2048, 1 % of K entries +-8, with max/mean-abs error vs
+  the fp32 oracle on row subsets), config 4 (whole prefills at L=32768 and
+  131072, chunk 2048, sparse vs dense) and config 5 (36 layers through the
+  plan / router layer, reference gates vs all dense, with the counters).
 
 ``--gpus N`` with N > 1 is refused: this build runs on one GPU.
 
-Other workloads (not the headline line; one JSON line each):
-
-* ``--workload config1`` -- the reference's CPU-runnable case: one launch,
-  rows 2357..2868 of a 2869-token prompt (384 sparse rows and the 128-row
-  dense tail);
-
-* ``--workload config3`` -- L=8320 in chunks of 2048 with 1 % of the K
-  entries set to +-8 (the same legs as above);
-* ``--workload config4`` -- long-context curve, chunk 2048: the whole prefill
-  as one HIP graph, sparse vs dense, for L from 1024 to 131072, and the
-  crossover L;
-* ``--workload config5`` -- 36 layers of config 2 through the plan / router
-  layer (layers 5, 7, 10, 15-35 sparse), eager, with the counter snapshot.
+Detailed single-workload runs (one JSON line each, not the headline):
+``--workload config1 | config3`` (same legs as the headline, that chunk set),
+``--workload config4`` (the whole long-context curve, L = 1024 .. 131072, and
+the crossover), ``--workload config5`` (the layer stack with the MI355X
+gate profile, the structured counter log and the vLLM-ROCm seam).
 """
 
 from __future__ import annotations
@@ -73,6 +75,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--chunk", type=int, default=512)
     ap.add_argument("--seed", type=int, default=7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-legs", action="store_true", help="headline only (skip the config 1/3/4/5 legs)")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--only", choices=("sparse", "dense"), help="run one kernel only (for profiling)")
     ap.add_argument("--workload", choices=("config1", "config2", "config3", "config4", "config5"),
@@ -93,119 +96,91 @@ def main() -> int:
     import torch
 
     from trianglemix import native
-    from trianglemix.workload import (SCALE, Chunk, chunk_bytes, chunk_flops, executed_flops, kv_bytes,
-                                      make_cache, make_query, prompt_chunks)
 
     if args.workload == "config4":
         return config4_curve(args)
     if args.workload == "config5":
         return config5_stack(args)
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    native.load_hip_library()
+    native.load_triangle_mix_adapter()
     headline = args.workload == "config2" and args.prompt == 8192 and args.chunk == 512 and not args.outliers
     if args.workload == "config3":
         args.prompt, args.chunk = 8320, 2048
         args.outliers = 0.01 if args.outliers is None else args.outliers
-    assert torch.cuda.is_available(), "bench.py needs a GPU"
-    native.load_hip_library()
-    native.load_triangle_mix_adapter()
-    dev = torch.device("cuda:0")
     if args.workload == "config1":
         args.prompt, args.chunk = 2869, 512
-        chunks = [Chunk(2357, 2869, 2869)]
-    else:
-        chunks = prompt_chunks(args.prompt, args.chunk)
+    line = chunk_set_line(args, headline)
+    if headline and args.only is None and not args.no_legs:
+        line["legs"] = headline_legs(args)
+    print(json.dumps(line), flush=True)
+    return 0
 
+
+def timing_stats(window_ms: list[float]) -> dict:
+    """Median, inter-quartile range, p10 and Tukey-fence outliers of per-window ms/step (as the reference
+    reports its cells, harness/npu_harness_common.py:663-722)."""
+    xs = sorted(window_ms)
+    n = len(xs)
+
+    def q(f):  # linear interpolation between closest ranks
+        pos = f * (n - 1)
+        lo = int(pos)
+        hi = min(lo + 1, n - 1)
+        return xs[lo] + (xs[hi] - xs[lo]) * (pos - lo)
+
+    q1, q3 = q(0.25), q(0.75)
+    iqr = q3 - q1
+    return {"windows": n, "median_ms": round(statistics.median(xs), 5), "q1_ms": round(q1, 5),
+            "q3_ms": round(q3, 5), "iqr_ms": round(iqr, 5), "p10_ms": round(q(0.10), 5),
+            "tukey_outliers": sum(1 for x in xs if x < q1 - 1.5 * iqr or x > q3 + 1.5 * iqr)}
+
+
+def abba(run_a, run_b, steps: int, windows: int):
+    """Time ``steps`` calls of run_a and of run_b in ``windows`` windows each, alternating A B B A A B ...;
+    every window is bracketed by events and a device synchronisation.  Returns (total ms of A, per-window
+    ms/step of A, total ms of B, per-window ms/step of B)."""
+    import torch
+
+    windows = max(2, min(windows, steps))
+    sizes = [steps // windows + (1 if i < steps % windows else 0) for i in range(windows)]
+    out = {"a": [0.0, []], "b": [0.0, []]}
+
+    def window(run, n, key):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(n):
+            run()
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e)
+        out[key][0] += ms
+        out[key][1].append(ms / n)
+
+    for i, n in enumerate(sizes):
+        order = (("a", run_a), ("b", run_b)) if i % 2 == 0 else (("b", run_b), ("a", run_a))
+        for key, run in order:
+            if run is not None:
+                window(run, n, key)
+    return out["a"][0], out["a"][1], out["b"][0], out["b"][1]
+
+
+def chunk_set_line(args, headline: bool) -> dict:
+    """The JSON line of one chunk set (config 2 by default; config 1 or 3 with --workload)."""
+    import torch
+
+    from trianglemix.workload import (SCALE, Chunk, chunk_bytes, chunk_flops, executed_flops, kv_bytes,
+                                      make_cache, make_query, prompt_chunks)
+
+    dev = torch.device("cuda:0")
+    chunks = [Chunk(2357, 2869, 2869)] if args.workload == "config1" else prompt_chunks(args.prompt, args.chunk)
     k, v, bt = make_cache(args.prompt, args.seed, std=1.0, outlier_frac=args.outliers or 0.0)
     qfull = make_query(args.prompt, args.seed + 1, std=1.0)
     kd, vd, btd = k.to(dev), v.to(dev), bt.to(dev)
-    qs = [qfull[c.query_start:c.seq_len].contiguous().to(dev) for c in chunks]
-    outs = [torch.empty_like(q) for q in qs]
-    sparse_op = torch.ops.trianglemix.triangle_paged_sparse_attention.out
-    dense_op = torch.ops.trianglemix.dense_paged_causal_attention.out
-
-    def sparse_step():
-        for c, q, o in zip(chunks, qs, outs):
-            sparse_op(q, kd, vd, btd, c.query_start, c.seq_len, c.prompt_len, SCALE, out=o)
-
-    def dense_step():
-        for c, q, o in zip(chunks, qs, outs):
-            dense_op(q, kd, vd, btd, c.query_start, c.seq_len, SCALE, out=o)
-
-    # Eager reference results for the graph replay checks.
-    sparse_step()
-    torch.cuda.synchronize()
-    eager_sparse = [o.clone() for o in outs]
-    dense_step()
-    torch.cuda.synchronize()
-    eager_dense = [o.clone() for o in outs]
-
-    def make_runner(step, reference):
-        if args.no_graph:
-            return step
-        graph = torch.cuda.CUDAGraph()
-        stream = torch.cuda.Stream()
-        stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(stream):
-            step()  # warm the allocator on the capture stream
-            torch.cuda.synchronize()
-            with torch.cuda.graph(graph, stream=stream):
-                step()
-        torch.cuda.current_stream().wait_stream(stream)
-        torch.cuda.synchronize()
-        for _ in range(3):  # every replay must reproduce the eager result
-            for o in outs:
-                o.zero_()
-            graph.replay()
-            torch.cuda.synchronize()
-            for o, ref in zip(outs, reference):
-                if not torch.equal(o, ref):
-                    raise RuntimeError("graph replay differs from eager launches")
-        return graph.replay
-
-    run_sparse = make_runner(sparse_step, eager_sparse)
-    run_dense = make_runner(dense_step, eager_dense)
-
-    def timed(run, steps):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(steps):
-            run()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / steps  # ms per step
-
-    for _ in range(args.warmup):
-        if args.only != "dense":
-            run_sparse()
-        if args.only != "sparse":
-            run_dense()
-    torch.cuda.synchronize()
-
-    # ABBA: sparse, dense, dense, sparse -- the timed region is the 2K sparse steps.
-    sparse_ms, dense_ms = [], []
-    half = max(1, args.steps // 2)
-    for order in ("sd", "ds"):
-        for which in order:
-            if which == "s" and args.only != "dense":
-                sparse_ms.append(timed(run_sparse, half))
-            if which == "d" and args.only != "sparse":
-                dense_ms.append(timed(run_dense, half))
-    ms_sparse = statistics.mean(sparse_ms) if sparse_ms else float("nan")
-    ms_dense = statistics.mean(dense_ms) if dense_ms else float("nan")
-
-    # Per-chunk kernel durations (eager, R back-to-back launches per chunk).
-    per_chunk_us = []
-    if args.only != "dense":
-        reps = 20
-        for c, q, o in zip(chunks, qs, outs):
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(reps):
-                sparse_op(q, kd, vd, btd, c.query_start, c.seq_len, c.prompt_len, SCALE, out=o)
-            e.record()
-            torch.cuda.synchronize()
-            per_chunk_us.append(round(s.elapsed_time(e) * 1000.0 / reps, 2))
-
+    m = measure_chunk_set(chunks, qfull, kd, vd, btd, args.steps, args.warmup, graph=not args.no_graph,
+                          only=args.only, per_chunk=True)
+    ms_sparse, ms_dense = m["ms_sparse"], m["ms_dense"]
     n = len(chunks)
     alg_flops = sum(chunk_flops(c) for c in chunks)
     exe_flops = sum(executed_flops(c) for c in chunks)
@@ -224,9 +199,10 @@ def main() -> int:
         del src, dst
 
     traffic = read_traffic_summary() if headline else None
-
     kv_write = kv_write_bench(args, chunks, k, v, bt, dev) if args.only is None and headline else None
-
+    errors = None
+    if args.workload == "config3" and args.only is None:
+        errors = oracle_errors(chunks, qfull, k, v, bt, m["outputs"])
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
         cpu = cpu_baseline(chunks, qfull, k, v, bt, SCALE)
@@ -239,7 +215,7 @@ def main() -> int:
     if args.workload == "config3":
         workload = (f"config3: one request, L={args.prompt}, chunked prefill {args.chunk} x {n} chunks, "
                     f"{args.outliers:.0%} of K entries +-8, Hq=32 Hkv=8 D=128 page=128, one layer")
-    line = {
+    return {
         "metric": METRIC if headline else f"sparse-prefill attn µs/chunk + MFMA %peak ({args.workload})",
         "value": round(us_per_chunk, 3),
         "unit": "us/chunk",
@@ -254,8 +230,10 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) bf16 Q/K/V, random page table)",
         "config": {
             "workload": workload,
-            "timing": f"HIP-graph replay of the {n} launches" if not args.no_graph else "eager launches",
+            "timing": (f"HIP-graph replay of the {n} launches" if not args.no_graph else "eager launches")
+                      + f"; {args.steps} timed steps in ABBA windows with the dense companion",
         },
+        "timing": m["sparse_stats"],
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved_tflops, 2),
@@ -266,20 +244,148 @@ def main() -> int:
             "alg_flops_per_launch": alg_flops // n,
             "alg_bytes_per_launch": alg_bytes // n,
             "executed_tile_tflops": round(exe_flops / (ms_sparse * 1e-3) / 1e12, 2),
+            "executed_tile_frac": round(exe_flops / (ms_sparse * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "kv_hbm_gbs": round(kvb / (ms_sparse * 1e-3) / 1e9, 1),
         },
-        "per_chunk_us": per_chunk_us,
+        "per_chunk_us": m["per_chunk_us"],
         "dense": {
             "ms_per_step": round(ms_dense, 5),
             "us_per_chunk": round(ms_dense * 1000.0 / n, 3),
             "alg_tflops": round(dense_flops / (ms_dense * 1e-3) / 1e12, 2) if ms_dense == ms_dense else None,
             "attention_time_cut": round(1.0 - ms_sparse / ms_dense, 4) if ms_dense == ms_dense else None,
+            "timing": m["dense_stats"],
         },
+        "errors_vs_fp32": errors,
         "kv_write": kv_write,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
-    return 0
+
+
+def measure_chunk_set(chunks, qfull, kd, vd, btd, steps, warmup, *, graph=True, only=None, per_chunk=False):
+    """Sparse vs dense over one chunk set: every chunk launch of a step captured in one HIP graph (each
+    replay checked against the eager result), ``warmup`` untimed steps, then ``steps`` timed steps of each
+    in ABBA windows.  Returns ms/step means, window statistics, eager per-chunk µs and the sparse outputs."""
+    import torch
+
+    from trianglemix.workload import SCALE
+
+    dev = kd.device
+    qs = [qfull[c.query_start:c.seq_len].contiguous().to(dev) for c in chunks]
+    outs = [torch.empty_like(q) for q in qs]
+    sparse_op = torch.ops.trianglemix.triangle_paged_sparse_attention.out
+    dense_op = torch.ops.trianglemix.dense_paged_causal_attention.out
+
+    def sparse_step():
+        for c, q, o in zip(chunks, qs, outs):
+            sparse_op(q, kd, vd, btd, c.query_start, c.seq_len, c.prompt_len, SCALE, out=o)
+
+    def dense_step():
+        for c, q, o in zip(chunks, qs, outs):
+            dense_op(q, kd, vd, btd, c.query_start, c.seq_len, SCALE, out=o)
+
+    sparse_step()
+    torch.cuda.synchronize()
+    eager_sparse = [o.clone() for o in outs]
+    dense_step()
+    torch.cuda.synchronize()
+    eager_dense = [o.clone() for o in outs]
+
+    def make_runner(step, reference):
+        if not graph:
+            return step
+        g = graph_of(step)
+        for _ in range(3):  # every replay must reproduce the eager result
+            for o in outs:
+                o.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            for o, ref in zip(outs, reference):
+                if not torch.equal(o, ref):
+                    raise RuntimeError("graph replay differs from eager launches")
+        return g.replay
+
+    run_sparse = make_runner(sparse_step, eager_sparse) if only != "dense" else None
+    run_dense = make_runner(dense_step, eager_dense) if only != "sparse" else None
+    for _ in range(warmup):
+        if run_sparse:
+            run_sparse()
+        if run_dense:
+            run_dense()
+    torch.cuda.synchronize()
+    windows = max(2, min(10, steps // 5 * 2))
+    tot_s, win_s, tot_d, win_d = abba(run_sparse, run_dense, steps, windows)
+    ms_sparse = tot_s / steps if win_s else float("nan")
+    ms_dense = tot_d / steps if win_d else float("nan")
+
+    per_chunk_us = []
+    if per_chunk and only != "dense":  # eager, 20 back-to-back launches per chunk
+        for c, q, o in zip(chunks, qs, outs):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(20):
+                sparse_op(q, kd, vd, btd, c.query_start, c.seq_len, c.prompt_len, SCALE, out=o)
+            e.record()
+            torch.cuda.synchronize()
+            per_chunk_us.append(round(s.elapsed_time(e) * 1000.0 / 20, 2))
+    return {"ms_sparse": ms_sparse, "ms_dense": ms_dense,
+            "sparse_stats": timing_stats(win_s) if win_s else None,
+            "dense_stats": timing_stats(win_d) if win_d else None,
+            "per_chunk_us": per_chunk_us, "outputs": eager_sparse}
+
+
+def oracle_errors(chunks, qfull, k, v, bt, outs, rows: int = 32) -> dict:
+    """max / mean-abs error vs the fp32 oracle on the first and last ``rows`` rows of every chunk."""
+    import numpy as np
+
+    from oracle.attention import attention_torch, error_metrics
+    from trianglemix.workload import SCALE
+
+    worst = {"max_abs": 0.0, "mean_abs": 0.0}
+    checked = 0
+    for c, o in zip(chunks, outs):
+        n = c.query_tokens
+        for r0, r1 in sorted({(0, min(rows, n)), (max(0, n - rows), n)}):
+            exp = attention_torch(qfull[c.query_start + r0:c.query_start + r1], k, v, bt, c.query_start + r0,
+                                  c.seq_len, c.prompt_len, SCALE)
+            m = error_metrics(o[r0:r1].float().cpu().numpy(), exp.float().numpy())
+            worst["max_abs"] = max(worst["max_abs"], m["max_abs"])
+            worst["mean_abs"] = max(worst["mean_abs"], m["mean_abs"])
+            checked += r1 - r0
+    return {"max_abs": float(np.float32(worst["max_abs"])), "worst_window_mean_abs": worst["mean_abs"],
+            "rows_checked": checked, "tolerance": {"max_abs": 2e-2, "mean_abs": 2e-3}}
+
+
+def headline_legs(args) -> dict:
+    """BASELINE configs 1, 3, 4 (L = 32768, 131072) and 5, measured after the headline (bounded)."""
+    import torch
+
+    from trianglemix.workload import Chunk, chunk_flops, executed_flops, make_cache, make_query, prompt_chunks
+
+    dev = torch.device("cuda:0")
+    legs = {}
+    for name, prompt, chunk, outliers in (("config1", 2869, 512, 0.0), ("config3", 8320, 2048, 0.01)):
+        chunks = [Chunk(2357, 2869, 2869)] if name == "config1" else prompt_chunks(prompt, chunk)
+        k, v, bt = make_cache(prompt, args.seed, std=1.0, outlier_frac=outliers)
+        qfull = make_query(prompt, args.seed + 1, std=1.0)
+        m = measure_chunk_set(chunks, qfull, k.to(dev), v.to(dev), bt.to(dev), 20, 5, per_chunk=True)
+        n = len(chunks)
+        flops = sum(chunk_flops(c) for c in chunks)
+        leg = {"us_per_chunk": round(m["ms_sparse"] * 1000.0 / n, 3),
+               "per_chunk_us": m["per_chunk_us"],
+               "mfma_frac": round(flops / (m["ms_sparse"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+               "executed_tile_frac": round(sum(executed_flops(c) for c in chunks) / (m["ms_sparse"] * 1e-3) / 1e12
+                                           / PEAK_BF16_TFLOPS, 4),
+               "dense_us_per_chunk": round(m["ms_dense"] * 1000.0 / n, 3),
+               "attention_time_cut": round(1.0 - m["ms_sparse"] / m["ms_dense"], 4),
+               "timing": m["sparse_stats"]}
+        if name == "config3":
+            leg["errors_vs_fp32"] = oracle_errors(chunks, qfull, k, v, bt, m["outputs"])
+        legs[name] = leg
+        del m
+        torch.cuda.empty_cache()
+    legs["config4"] = long_context_points(args.seed, (32768, 131072))
+    legs["config5"] = layer_stack_summary(args.seed)
+    return legs
 
 
 def graph_of(step):
@@ -315,22 +421,19 @@ def median_ms(run, reps: int, windows: int = 3) -> float:
     return statistics.median(times)
 
 
-def config4_curve(args) -> int:
-    """Long-context curve (chunk 2048): whole-prefill sparse vs dense attention time per L, and the crossover."""
+def long_context_points(seed: int, lengths) -> list[dict]:
+    """Whole prefills (chunk 2048), sparse vs dense, one HIP graph of the chunk launches per L; ABBA windows."""
     import torch
 
-    from trianglemix import native
     from trianglemix.workload import SCALE, chunk_flops, prompt_chunks
 
-    native.load_hip_library()
-    native.load_triangle_mix_adapter()
     dev = torch.device("cuda:0")
     sparse_op = torch.ops.trianglemix.triangle_paged_sparse_attention.out
     dense_op = torch.ops.trianglemix.dense_paged_causal_attention.out
     chunk = 2048
     curve = []
-    for L in (1024, 2048, 4096, 8192, 16384, 32768, 131072):
-        g = torch.Generator(device=dev).manual_seed(args.seed + L)
+    for L in lengths:
+        g = torch.Generator(device=dev).manual_seed(seed + L)
         logical = (L + 127) // 128
         pages = logical + 7
         table = torch.randperm(pages, generator=g, device=dev)[:logical].to(torch.int32).view(1, -1)
@@ -351,19 +454,33 @@ def config4_curve(args) -> int:
                          out=out[c.query_start:c.seq_len])
 
         gs, gd = graph_of(sparse_step), graph_of(dense_step)
-        reps = 2 if L >= 131072 else (5 if L >= 32768 else 20)
-        ms_s = statistics.mean([median_ms(gs.replay, reps), median_ms(gs.replay, reps)])  # A B B A
-        ms_d = statistics.mean([median_ms(gd.replay, reps), median_ms(gd.replay, reps)])
+        gs.replay()
+        gd.replay()
+        reps = 4 if L >= 131072 else (10 if L >= 32768 else 40)
+        tot_s, win_s, tot_d, win_d = abba(gs.replay, gd.replay, reps, 4)
+        ms_s, ms_d = tot_s / reps, tot_d / reps
         fs = sum(chunk_flops(c) for c in chunks)
         fd = sum(chunk_flops(c, dense=True) for c in chunks)
         curve.append({"L": L, "chunks": len(chunks), "sparse_ms": round(ms_s, 4), "dense_ms": round(ms_d, 4),
                       "speedup": round(ms_d / ms_s, 3), "sparse_gflop": round(fs / 1e9, 2),
                       "dense_gflop": round(fd / 1e9, 2), "sparse_tflops": round(fs / (ms_s * 1e-3) / 1e12, 1),
-                      "dense_tflops": round(fd / (ms_d * 1e-3) / 1e12, 1)})
+                      "dense_tflops": round(fd / (ms_d * 1e-3) / 1e12, 1),
+                      "sparse_us_per_chunk": round(ms_s * 1000.0 / len(chunks), 2),
+                      "sparse_window_iqr_ms": timing_stats(win_s)["iqr_ms"]})
         print(f"# config4 L={L}: sparse {ms_s:.3f} ms dense {ms_d:.3f} ms x{ms_d / ms_s:.2f}", file=sys.stderr,
               flush=True)
         del kc, vc, q, out, gs, gd
         torch.cuda.empty_cache()
+    return curve
+
+
+def config4_curve(args) -> int:
+    """Long-context curve (chunk 2048): whole-prefill sparse vs dense attention time per L, and the crossover."""
+    from trianglemix import native
+
+    native.load_hip_library()
+    native.load_triangle_mix_adapter()
+    curve = long_context_points(args.seed, (1024, 2048, 4096, 8192, 16384, 32768, 131072))
     wins = [p["L"] for p in curve if p["sparse_ms"] < p["dense_ms"]]
     line = {
         "metric": "long-context prefill attention, sparse vs dense (config4, chunk 2048)",
@@ -508,83 +625,149 @@ def vllm_seam_stack(qs, kcs, vcs, table, chunks, selected: str, prompt_len: int)
     return result
 
 
-def config5_stack(args) -> int:
-    """36 layers x config 2 through the plan / router layer; counters from the stats snapshot."""
-    import torch
+class LayerStack:
+    """36 attention layers at config-2 geometry (own Q / K / V per layer, one random page table), prefilled
+    chunk by chunk through the plan / router layer."""
 
-    from trianglemix import native
-    from trianglemix.config import resolve_plugin_config
-    from trianglemix.counters import aggregate as counters_aggregate
-    from trianglemix.counters import report_status, scan_events
-    from trianglemix.planning import build_batch_plan
-    from trianglemix.router import TriangleMixRouter
-    from trianglemix.stats import TriangleMixRuntimeStats
-    from trianglemix.workload import SCALE, chunk_flops, prompt_chunks
+    L, CHUNK, LAYERS, SELECTED = 8192, 512, 36, "5,7,10,15-35"
 
-    native.load_hip_library()
-    native.load_triangle_mix_adapter()
-    dev = torch.device("cuda:0")
-    L, chunk, layers = 8192, 512, 36
-    selected = "5,7,10,15-35"
-    g = torch.Generator(device=dev).manual_seed(args.seed)
-    logical = L // 128
-    pages = logical + 7
-    table = torch.randperm(pages, generator=g, device=dev)[:logical].to(torch.int32).view(1, -1)
-    kcs = [torch.randn(pages, 128, 8, 128, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
-    vcs = [torch.randn(pages, 128, 8, 128, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
-    qs = [torch.randn(L, 32, 128, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
-    outs = [torch.empty_like(x) for x in qs]
-    chunks = prompt_chunks(L, chunk)
+    def __init__(self, seed: int):
+        import torch
 
-    class _Vllm:
-        def __init__(self, enabled, profile="", log_interval=0):
-            section = {"enabled": enabled, "layers": selected, "stats_log_interval": log_interval}
-            if profile:
-                section["gate_profile"] = profile
-            self.additional_config = {"trianglemix": section}
+        from trianglemix.workload import prompt_chunks
 
-    class _Lines(logging.Handler):
-        def __init__(self):
-            super().__init__()
-            self.lines = []
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev).manual_seed(seed)
+        logical = self.L // 128
+        pages = logical + 7
+        self.table = torch.randperm(pages, generator=g, device=dev)[:logical].to(torch.int32).view(1, -1)
+        shape = (pages, 128, 8, 128)
+        self.kcs = [torch.randn(shape, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(self.LAYERS)]
+        self.vcs = [torch.randn(shape, generator=g, device=dev, dtype=torch.bfloat16) for _ in range(self.LAYERS)]
+        self.qs = [torch.randn(self.L, 32, 128, generator=g, device=dev, dtype=torch.bfloat16)
+                   for _ in range(self.LAYERS)]
+        self.outs = [torch.empty_like(x) for x in self.qs]
+        self.chunks = prompt_chunks(self.L, self.CHUNK)
 
-        def emit(self, record):
-            self.lines.append(record.getMessage())
+    def config(self, enabled: bool, profile: str = "", log_interval: int = 0):
+        from trianglemix.config import resolve_plugin_config
 
-    def run_prefill(router, cfg):
-        for c in chunks:
+        section = {"enabled": enabled, "layers": self.SELECTED, "stats_log_interval": log_interval}
+        if profile:
+            section["gate_profile"] = profile
+
+        class _Vllm:
+            additional_config = {"trianglemix": section}
+
+        return resolve_plugin_config(_Vllm())
+
+    def prefill(self, router, cfg) -> None:
+        from trianglemix.planning import build_batch_plan
+        from trianglemix.workload import SCALE
+
+        for c in self.chunks:
             plan = build_batch_plan(state_name="ChunkedPrefill", cumulative_query_ends=[c.query_tokens],
-                                    seq_lens=[c.seq_len], prompt_lens=[L], num_decodes=0, num_prefills=1,
+                                    seq_lens=[c.seq_len], prompt_lens=[self.L], num_decodes=0, num_prefills=1,
                                     config=cfg.kernel)
-            for i in range(layers):
+            for i in range(self.LAYERS):
                 router.prefill_attention(layer_name=f"model.layers.{i}.self_attn.attn", plan=plan,
-                                         query=qs[i][c.query_start:c.seq_len], key_cache=kcs[i], value_cache=vcs[i],
-                                         block_table=table, output=outs[i][c.query_start:c.seq_len],
-                                         softmax_scale=SCALE)
+                                         query=self.qs[i][c.query_start:c.seq_len], key_cache=self.kcs[i],
+                                         value_cache=self.vcs[i], block_table=self.table,
+                                         output=self.outs[i][c.query_start:c.seq_len], softmax_scale=SCALE)
 
-    results = {}
-    router_log = logging.getLogger("trianglemix.router")
-    for name, enabled, profile, interval in (("trianglemix", True, "", 0),
-                                             ("trianglemix_mi355x_gates", True, "mi355x", 0),
-                                             ("all_dense", False, "", 0),
-                                             ("trianglemix_logged", True, "", len(chunks))):
-        cfg = resolve_plugin_config(_Vllm(enabled, profile, interval))
-        stats = TriangleMixRuntimeStats()
-        router = TriangleMixRouter(cfg, stats=stats)
-        run_prefill(router, cfg)  # warm-up
-        torch.cuda.synchronize()
-        stats.snapshot(reset=True)
-        handler = _Lines()
-        router_log.addHandler(handler)
+    def run(self, variants, windows: int = 3) -> dict:
+        """ms per prefill (median of ``windows``, variants interleaved A B .. B A), stats snapshot and router
+        log lines of each (name, enabled, gate profile, stats_log_interval) variant."""
+        import torch
+
+        from trianglemix.router import TriangleMixRouter
+        from trianglemix.stats import TriangleMixRuntimeStats
+
+        class _Lines(logging.Handler):
+            def __init__(self):
+                super().__init__()
+                self.lines = []
+
+            def emit(self, record):
+                self.lines.append(record.getMessage())
+
+        state = {}
+        for name, enabled, profile, interval in variants:
+            cfg = self.config(enabled, profile, interval)
+            stats = TriangleMixRuntimeStats()
+            router = TriangleMixRouter(cfg, stats=stats)
+            self.prefill(router, cfg)  # warm-up
+            torch.cuda.synchronize()
+            stats.snapshot(reset=True)
+            state[name] = (cfg, stats, router, _Lines(), [])
+        router_log = logging.getLogger("trianglemix.router")
         level = router_log.level
         router_log.setLevel(logging.INFO)
         try:
-            ms = median_ms(lambda: run_prefill(router, cfg), 1)
+            names = [v[0] for v in variants]
+            for w in range(windows):
+                for name in (names if w % 2 == 0 else names[::-1]):
+                    cfg, stats, router, handler, times = state[name]
+                    router_log.addHandler(handler)
+                    try:
+                        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        torch.cuda.synchronize()
+                        s.record()
+                        self.prefill(router, cfg)
+                        e.record()
+                        torch.cuda.synchronize()
+                        times.append(s.elapsed_time(e))
+                    finally:
+                        router_log.removeHandler(handler)
         finally:
-            router_log.removeHandler(handler)
             router_log.setLevel(level)
-        snap = stats.snapshot(reset=False)
-        results[name] = {"ms_per_prefill": round(ms, 3), "stats": snap, "log_lines": handler.lines}
+        return {name: {"ms_per_prefill": round(statistics.median(times), 3), "windows_ms": [round(t, 3) for t in times],
+                       "stats": stats.snapshot(reset=False), "log_lines": handler.lines}
+                for name, (cfg, stats, router, handler, times) in state.items()}
+
+
+def layer_stack_summary(seed: int) -> dict:
+    """Config 5 leg of the default run: reference gates vs every layer dense, with the counters."""
+    import torch
+
+    from trianglemix.workload import chunk_flops
+
+    stack = LayerStack(seed)
+    res = stack.run((("trianglemix", True, "", 0), ("all_dense", False, "", 0)))
+    sel = stack.config(True).kernel.layer_indices
+    tm = res["trianglemix"]["stats"]
+    out = {
+        "workload": f"L={stack.L}, chunked prefill {stack.CHUNK} x {len(stack.chunks)}, {stack.LAYERS} layers, "
+                    f"layers {stack.SELECTED} sparse, reference gates; eager, median of 3 interleaved prefills",
+        "ms_per_prefill": res["trianglemix"]["ms_per_prefill"],
+        "all_dense_ms_per_prefill": res["all_dense"]["ms_per_prefill"],
+        "attention_time_cut": round(1 - res["trianglemix"]["ms_per_prefill"] / res["all_dense"]["ms_per_prefill"], 4),
+        "gflop": {"routed": round(sum(chunk_flops(c, dense=(i not in sel)) for c in stack.chunks
+                                      for i in range(stack.LAYERS)) / 1e9, 1),
+                  "all_dense": round(sum(chunk_flops(c, dense=True) for c in stack.chunks) * stack.LAYERS / 1e9, 1)},
+        "counters": {k: v for k, v in tm["counters"].items() if not k.endswith("_ns")},
+        "fallback_reasons": tm["fallback_reasons"],
+    }
+    del stack
+    torch.cuda.empty_cache()
+    return out
+
+
+def config5_stack(args) -> int:
+    """36 layers x config 2 through the plan / router layer; counters from the stats snapshot."""
+    from trianglemix import native
+    from trianglemix.counters import aggregate as counters_aggregate
+    from trianglemix.counters import report_status, scan_events
+    from trianglemix.workload import chunk_flops
+
+    native.load_hip_library()
+    native.load_triangle_mix_adapter()
+    stack = LayerStack(args.seed)
+    chunks, L, layers = stack.chunks, stack.L, stack.LAYERS
+    results = stack.run((("trianglemix", True, "", 0),
+                         ("trianglemix_mi355x_gates", True, "mi355x", 0),
+                         ("all_dense", False, "", 0),
+                         ("trianglemix_logged", True, "", len(chunks))), windows=1)
     # the structured log of the logged run, aggregated the way a run's worker logs are
     logged = results["trianglemix_logged"]
     report = counters_aggregate(scan_events("\n".join(logged["log_lines"]), source="config5"))
@@ -597,7 +780,7 @@ def config5_stack(args) -> int:
         "ms_per_prefill": logged["ms_per_prefill"],
         "logging_overhead": round(logged["ms_per_prefill"] / results["trianglemix"]["ms_per_prefill"] - 1, 4),
     }
-    sel = resolve_plugin_config(_Vllm(True)).kernel.layer_indices
+    sel = stack.config(True).kernel.layer_indices
     gflop = sum(chunk_flops(c, dense=(i not in sel)) for c in chunks for i in range(layers)) / 1e9
     dense_gflop = sum(chunk_flops(c, dense=True) for c in chunks) * layers / 1e9
     tm = results["trianglemix"]["stats"]
@@ -609,8 +792,8 @@ def config5_stack(args) -> int:
         "higher_is_better": False,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 Q/K/V per layer from the GPU generator, random page table)",
-        "config": {"workload": f"config5: L={L}, chunked prefill {chunk} x {len(chunks)}, {layers} layers, "
-                               f"layers {selected} sparse", "gates": "reference defaults"},
+        "config": {"workload": f"config5: L={L}, chunked prefill {stack.CHUNK} x {len(chunks)}, {layers} layers, "
+                               f"layers {stack.SELECTED} sparse", "gates": "reference defaults"},
         "all_dense_ms_per_prefill": results["all_dense"]["ms_per_prefill"],
         "mi355x_gates": {
             "ms_per_prefill": results["trianglemix_mi355x_gates"]["ms_per_prefill"],
@@ -626,7 +809,7 @@ def config5_stack(args) -> int:
         "fallback_reasons": tm["fallback_reasons"],
         "routing": tm["performance"],
         "structured_log": structured_log,
-        "vllm_seam": vllm_seam_stack(qs, kcs, vcs, table, chunks, selected, L),
+        "vllm_seam": vllm_seam_stack(stack.qs, stack.kcs, stack.vcs, stack.table, chunks, stack.SELECTED, L),
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -698,30 +881,33 @@ def read_traffic_summary():
 
 
 def cpu_baseline(chunks, qfull, k, v, bt, scale):
-    """fp32 PyTorch CPU oracle over all chunks (bounded: ~2 passes of ~6 s)."""
+    """fp32 PyTorch CPU oracle over all chunks on every core of this host: one warm-up pass, median of 3."""
     import torch
 
     from oracle.attention import attention_torch
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    mid = chunks[len(chunks) // 2]
-    attention_torch(qfull[mid.query_start:mid.seq_len], k, v, bt, mid.query_start, mid.seq_len, mid.prompt_len,
-                    scale)  # warm-up
-    passes = []
-    for _ in range(2):
+    print(f"# cpu_baseline: torch.set_num_threads({threads}) (os.cpu_count()); "
+          f"{len(os.sched_getaffinity(0))} cores in this process's affinity mask", file=sys.stderr, flush=True)
+
+    def one_pass():
         t0 = time.perf_counter()
         for c in chunks:
-            attention_torch(qfull[c.query_start:c.seq_len], k, v, bt, c.query_start, c.seq_len, c.prompt_len,
-                            scale)
-        passes.append(time.perf_counter() - t0)
+            attention_torch(qfull[c.query_start:c.seq_len], k, v, bt, c.query_start, c.seq_len, c.prompt_len, scale)
+        return time.perf_counter() - t0
+
+    warm = one_pass()
+    passes = [one_pass() for _ in range(3)]
     per_chunk_us = statistics.median(passes) / len(chunks) * 1e6
     return {
         "value": round(per_chunk_us, 1),
         "unit": "us/chunk",
         "cores": threads,
         "kind": "port",
-        "sample": f"all {len(chunks)} chunks of the same workload, fp32 torch CPU oracle, median of 2 passes",
+        "sample": (f"all {len(chunks)} chunks of the same workload (same seeded inputs), fp32 torch CPU oracle; "
+                   f"one warm-up pass ({warm:.2f} s), then the median of 3 passes "
+                   f"({', '.join(f'{x:.2f}' for x in passes)} s)"),
     }
 
 

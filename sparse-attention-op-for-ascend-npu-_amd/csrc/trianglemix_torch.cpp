@@ -30,9 +30,13 @@
 // from PyTorch's caching allocator, as the reference's EXEC_NPU_CMD takes the
 // aclnn workspace from torch_npu's -- whose arrival counters are zeroed once
 // when it is created (the kernel leaves them zero).  Launches on one stream
-// run in order, so they share it; under stream capture each call gets a
-// buffer of its own from the capture's memory, with the counters cleared by a
-// captured fill.
+// run in order, so they share it.  A buffer, once handed out, stays alive
+// until the process ends (a larger one replaces it for later calls): a HIP
+// graph captured on a stream may keep using it on every replay.  Under
+// stream capture the stream's buffer is used when it is large enough;
+// otherwise the call gets a buffer of its own from the capture's memory, its
+// counters cleared by a captured fill.  A graph replayed on another stream
+// must not overlap other work on the capture stream's workspace.
 
 #include <ATen/ATen.h>
 #include <ATen/MemoryOverlap.h>
@@ -44,6 +48,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "../../include/trianglemix.h"
 
@@ -93,23 +98,23 @@ at::Tensor workspace_for(const at::Tensor& like, int64_t bytes, void* stream) {
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   TORCH_CHECK(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &capture) == hipSuccess,
               "hipStreamIsCapturing failed");
+  const bool capturing = capture != hipStreamCaptureStatusNone;
   const auto options = like.options().dtype(at::kByte);
-  if (capture != hipStreamCaptureStatusNone) {
+  static std::mutex mutex;
+  // Every buffer ever handed out, per (device, stream); the last is current.
+  static std::map<std::pair<int, void*>, std::vector<at::Tensor>> cache;
+  std::lock_guard<std::mutex> lock(mutex);
+  std::vector<at::Tensor>& held = cache[{like.device().index(), stream}];
+  if (!held.empty() && held.back().numel() >= bytes) return held.back();
+  if (capturing) {
     at::Tensor ws = at::empty({bytes}, options);
     ws.narrow(0, 0, TM_WORKSPACE_COUNTER_BYTES).zero_();
     return ws;
   }
-  static std::mutex mutex;
-  static std::map<std::pair<int, void*>, at::Tensor> cache;
-  std::lock_guard<std::mutex> lock(mutex);
-  at::Tensor& ws = cache[{like.device().index(), stream}];
-  if (!ws.defined() || ws.numel() < bytes) {
-    // Grow geometrically; the old buffer is released to the caching
-    // allocator, which reuses it only after the work queued on this stream.
-    const int64_t size = ws.defined() ? std::max(bytes, 2 * ws.numel()) : bytes;
-    ws = at::empty({size}, options);
-    ws.narrow(0, 0, TM_WORKSPACE_COUNTER_BYTES).zero_();
-  }
+  const int64_t size = held.empty() ? bytes : std::max(bytes, 2 * held.back().numel());
+  at::Tensor ws = at::empty({size}, options);
+  ws.narrow(0, 0, TM_WORKSPACE_COUNTER_BYTES).zero_();
+  held.push_back(ws);
   return ws;
 }
 

@@ -51,7 +51,9 @@ def workspace_size(query_tokens: int, query_start: int, seq_len: int, prompt_len
 # Split-KV workspace per (device, stream): the first WORKSPACE_COUNTER_BYTES
 # are arrival counters that must be zero before a workspace's first use (the
 # kernel leaves them zero), so a buffer is zero-filled once when created and
-# then kept -- alive for as long as work queued on its stream may use it.
+# then kept.  Every buffer handed out stays alive until the process ends (a
+# larger one replaces it for later calls), so work still queued on a stream,
+# or a graph captured on it, never sees its workspace freed.
 WORKSPACE_COUNTER_BYTES = 65536
 _WORKSPACES: dict = {}
 
@@ -63,13 +65,12 @@ def _workspace(query, query_start, seq_len, prompt_len, workspace, stream):
     if workspace is None:
         import torch
 
-        key = (query.device.index, int(stream))
-        workspace = _WORKSPACES.get(key)
-        if workspace is None or workspace.numel() < need:
-            size = need if workspace is None else max(need, 2 * workspace.numel())
+        held = _WORKSPACES.setdefault((query.device.index, int(stream)), [])
+        if not held or held[-1].numel() < need:
+            size = need if not held else max(need, 2 * held[-1].numel())
             with torch.cuda.stream(torch.cuda.ExternalStream(int(stream), device=query.device)):
-                workspace = torch.zeros(size, dtype=torch.uint8, device=query.device)
-            _WORKSPACES[key] = workspace
+                held.append(torch.zeros(size, dtype=torch.uint8, device=query.device))
+        workspace = held[-1]
     return workspace.data_ptr(), workspace.numel() * workspace.element_size()
 
 
