@@ -1,11 +1,17 @@
 """Typed TriangleMix configuration: additional_config > environment > defaults.
 
-Mirror of package/src/vllm_ascend_trianglemix/config.py: the same keys,
-precedence (``additional_config["trianglemix"]`` first, then the
-``VLLM_ASCEND_TRIANGLE_MIX_*`` environment variables kept as the
-compatibility interface, then defaults) and strict boolean coercion
-(:16-29).  The environment names are kept verbatim so existing deployments
-switch without edits.
+The keys, their precedence (``additional_config["trianglemix"]`` first --
+or the whole ``additional_config`` when it has no ``trianglemix`` section --
+then the ``VLLM_ASCEND_TRIANGLE_MIX_*`` environment variables, then defaults),
+the boolean spellings and the error messages are the reference's contract
+(package/src/vllm_ascend_trianglemix/config.py); the environment names are
+kept verbatim so existing deployments switch without edits.  Golden results
+of the reference for a set of inputs pin it (tests/test_policy_golden.py).
+
+Every setting is one ``_Setting`` row (key, environment variable,
+default, kind); ``_Source`` looks a row up in the section, then the
+environment, and parses it by kind.  Rows resolve in table order, so with
+several bad values the first row's error is the one raised.
 
 One key is this build's own: ``gate_profile`` (environment
 ``VLLM_ASCEND_TRIANGLE_MIX_GATE_PROFILE``) names a crossover profile measured
@@ -21,43 +27,25 @@ import json
 import os
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Any, Mapping
+from typing import Any, Mapping, NamedTuple
 
 from .kernel import TriangleMixConfig, parse_layer_indices
 
-_TRUE = frozenset({"1", "true", "yes", "on"})
-_FALSE = frozenset({"0", "false", "no", "off"})
+# Accepted spellings of a boolean (after strip + lower-case).
+_BOOL_WORDS = {"1": True, "true": True, "yes": True, "on": True,
+               "0": False, "false": False, "no": False, "off": False}
 
 
-def _coerce_bool(value: object, *, name: str) -> bool:
+def _as_bool(value: object, label: str) -> bool:
+    """``value`` as a boolean: a bool, the integers 0 / 1, or one of ``_BOOL_WORDS``; else ValueError."""
     if isinstance(value, bool):
         return value
     if isinstance(value, int) and value in (0, 1):
-        return bool(value)
-    if isinstance(value, str):
-        text = value.strip().lower()
-        if text in _TRUE:
-            return True
-        if text in _FALSE:
-            return False
-    raise ValueError(f"TriangleMix {name} must be a boolean, got {value!r}")
-
-
-def _mapping(value: object) -> Mapping[str, Any]:
-    return value if isinstance(value, Mapping) else {}
-
-
-def _value(section: Mapping[str, Any], name: str, env_name: str, default: Any) -> Any:
-    if name in section:
-        return section[name]
-    env = os.getenv(env_name)
-    if env is None:
-        return default
-    if isinstance(default, bool):
-        return _coerce_bool(env, name=env_name)
-    if isinstance(default, int):
-        return int(env)
-    return env
+        return value == 1
+    word = value.strip().lower() if isinstance(value, str) else None
+    if word in _BOOL_WORDS:
+        return _BOOL_WORDS[word]
+    raise ValueError(f"TriangleMix {label} must be a boolean, got {value!r}")
 
 
 @dataclass(frozen=True)
@@ -76,17 +64,68 @@ class PluginConfig:
 
 _ENV = "VLLM_ASCEND_TRIANGLE_MIX_"
 
-# (config key, environment variable, default, TriangleMixConfig field)
-_INT_KEYS = (
-    ("sink_tokens", _ENV + "SINK_TOKENS", 8, "sink_tokens"),
-    ("local_window", _ENV + "LOCAL_WINDOW", 512, "local_window"),
-    ("last_rows", _ENV + "LAST_ROWS", 128, "last_rows"),
-    ("min_seq_len", _ENV + "DIRECT_MIN_SEQ_LEN", 0, "direct_min_seq_len"),
-    ("min_sparse_rows", _ENV + "DIRECT_MIN_SPARSE_ROWS", 128, "direct_min_sparse_rows"),
-    ("min_saved_qk", _ENV + "DIRECT_MIN_SAVED_QK", 913_152, "direct_min_saved_qk"),
-    ("split_min_sparse_rows", _ENV + "DIRECT_SPLIT_MIN_SPARSE_ROWS", 192, "direct_split_min_sparse_rows"),
-    ("split_min_saved_qk", _ENV + "DIRECT_SPLIT_MIN_SAVED_QK", 1_299_264, "direct_split_min_saved_qk"),
+
+class _Setting(NamedTuple):
+    key: str                 # additional_config key
+    env: str                 # environment variable
+    default: Any
+    kind: str                # "bool", "int", "layers" or "text"
+    field: str | None = None  # TriangleMixConfig field, when the setting is one
+
+
+# Resolution order (the order errors surface in): the kernel settings, then the stats
+# settings, then ``strict``.
+_KERNEL_SETTINGS = (
+    _Setting("enabled", "VLLM_ASCEND_ENABLE_TRIANGLE_MIX", False, "bool", "enabled"),
+    _Setting("layers", _ENV + "LAYERS", "", "layers", "layer_indices"),
+    _Setting("sink_tokens", _ENV + "SINK_TOKENS", 8, "int", "sink_tokens"),
+    _Setting("local_window", _ENV + "LOCAL_WINDOW", 512, "int", "local_window"),
+    _Setting("last_rows", _ENV + "LAST_ROWS", 128, "int", "last_rows"),
+    _Setting("min_seq_len", _ENV + "DIRECT_MIN_SEQ_LEN", 0, "int", "direct_min_seq_len"),
+    _Setting("min_sparse_rows", _ENV + "DIRECT_MIN_SPARSE_ROWS", 128, "int", "direct_min_sparse_rows"),
+    _Setting("min_saved_qk", _ENV + "DIRECT_MIN_SAVED_QK", 913_152, "int", "direct_min_saved_qk"),
+    _Setting("split_min_sparse_rows", _ENV + "DIRECT_SPLIT_MIN_SPARSE_ROWS", 192, "int",
+             "direct_split_min_sparse_rows"),
+    _Setting("split_min_saved_qk", _ENV + "DIRECT_SPLIT_MIN_SAVED_QK", 1_299_264, "int",
+             "direct_split_min_saved_qk"),
 )
+_RECENT_CAPACITY = _Setting("stats_recent_capacity", _ENV + "STATS_RECENT_CAPACITY", 256, "int")
+_LOG_INTERVAL = _Setting("stats_log_interval", _ENV + "STATS_LOG_INTERVAL", 0, "int")
+_STRICT = _Setting("strict", _ENV + "STRICT", False, "bool")
+_GATE_PROFILE = _Setting("gate_profile", _ENV + "GATE_PROFILE", "", "text")
+
+
+class _Source:
+    """One ``additional_config`` section backed by the environment."""
+
+    def __init__(self, vllm_config: object | None) -> None:
+        additional = getattr(vllm_config, "additional_config", None)
+        additional = additional if isinstance(additional, Mapping) else {}
+        section = additional.get("trianglemix", additional)
+        self.section: Mapping[str, Any] = section if isinstance(section, Mapping) else {}
+
+    def get(self, setting: _Setting, default: Any = None) -> Any:
+        """The setting's value, parsed by kind.  Section values are taken as given, environment strings
+        are parsed first; ``default`` (when given) replaces the row's default."""
+        default = setting.default if default is None else default
+        if setting.key in self.section:
+            raw, label = self.section[setting.key], setting.key
+        elif setting.env in os.environ:
+            text = os.environ[setting.env]
+            # environment text becomes the default's type; errors name the variable
+            raw = (_as_bool(text, setting.env) if setting.kind == "bool"
+                   else int(text) if setting.kind == "int" else text)
+            label = setting.key
+        else:
+            raw, label = default, setting.key
+        if setting.kind == "bool":
+            return _as_bool(raw, label)
+        if setting.kind == "int":
+            return int(raw)
+        if setting.kind == "layers":
+            text = ",".join(str(x) for x in raw) if isinstance(raw, (list, tuple, set)) else str(raw)
+            return parse_layer_indices(text)
+        return raw
 
 
 _GATE_FIELDS = ("direct_min_seq_len", "direct_min_sparse_rows", "direct_min_saved_qk",
@@ -108,27 +147,13 @@ def load_gate_profile(name_or_path: str) -> dict[str, int]:
 
 
 def resolve_plugin_config(vllm_config: object | None) -> PluginConfig:
-    """Resolve typed config, preferring ``additional_config.trianglemix``."""
-    additional = _mapping(getattr(vllm_config, "additional_config", None))
-    section = _mapping(additional.get("trianglemix", additional))
-    layers = _value(section, "layers", _ENV + "LAYERS", "")
-    layers_text = ",".join(str(x) for x in layers) if isinstance(layers, (list, tuple, set)) else str(layers)
-    profile = str(_value(section, "gate_profile", _ENV + "GATE_PROFILE", "") or "")
+    """Resolve the typed configuration, preferring ``additional_config.trianglemix``."""
+    source = _Source(vllm_config)
+    profile = str(source.get(_GATE_PROFILE) or "")
     profile_gates = load_gate_profile(profile) if profile else {}
-    ints = {field: int(_value(section, key, env, profile_gates.get(field, default)))
-            for key, env, default, field in _INT_KEYS}
-    kernel = TriangleMixConfig(
-        enabled=_coerce_bool(_value(section, "enabled", "VLLM_ASCEND_ENABLE_TRIANGLE_MIX", False), name="enabled"),
-        layer_indices=parse_layer_indices(layers_text),
-        **ints,
-    )
-    recent = int(_value(section, "stats_recent_capacity", _ENV + "STATS_RECENT_CAPACITY", 256))
-    interval = int(_value(section, "stats_log_interval", _ENV + "STATS_LOG_INTERVAL", 0))
+    kernel = TriangleMixConfig(**{s.field: source.get(s, profile_gates.get(s.field)) for s in _KERNEL_SETTINGS})
+    recent, interval = source.get(_RECENT_CAPACITY), source.get(_LOG_INTERVAL)
     if recent < 0 or interval < 0:
         raise ValueError("TriangleMix stats capacities must be non-negative")
-    return PluginConfig(
-        kernel=kernel,
-        strict=_coerce_bool(_value(section, "strict", _ENV + "STRICT", False), name="strict"),
-        stats_recent_capacity=recent,
-        stats_log_interval=interval,
-    )
+    return PluginConfig(kernel=kernel, strict=source.get(_STRICT), stats_recent_capacity=recent,
+                        stats_log_interval=interval)

@@ -1,9 +1,10 @@
 """Per-scheduler-step routing plan: one immutable plan reused by every layer.
 
-Mirror of package/src/vllm_ascend_trianglemix/planning.py: the same 24
-``FallbackReason`` values (:14-38), plan records (:41-75), request gates in
-the same order (:86-116) and batch gates (:119-207).  The string values are
-the counter keys of ``stats.py`` and must not change.
+Contract shared with the reference (package/src/vllm_ascend_trianglemix/
+planning.py): the 24 ``FallbackReason`` values (:14-38) -- they are the
+counter keys of ``stats.py`` -- the plan records (:41-75), the request gates
+and their order (:86-116) and the batch gates (:119-207).  Golden plan records
+of the reference pin the behaviour (tests/test_policy_golden.py).
 """
 
 from __future__ import annotations
@@ -107,49 +108,60 @@ def _request_reason(*, query_len: int, seq_len: int, prompt_len: int,
     return span, FallbackReason.NONE
 
 
+def _batch_reason(state_name: str, ends: tuple[int, ...], seqs: tuple[int, ...], prompts: tuple[int, ...],
+                  num_decodes: int, num_prefills: int) -> FallbackReason:
+    """The first batch-level gate the step fails, in gate order (NONE when it passes all)."""
+    batch = len(seqs)
+    complete = bool(ends and seqs and prompts) and len(ends) == len(prompts) == num_prefills == batch
+    gates = (
+        (lambda: state_name not in PREFILL_STATES, FallbackReason.STATE_UNSUPPORTED),
+        (lambda: num_decodes != 0, FallbackReason.MIXED_DECODE),
+        (lambda: not complete, FallbackReason.MISSING_METADATA),
+        (lambda: batch != 1, FallbackReason.BATCH_UNSUPPORTED),
+    )
+    return next((reason for failed, reason in gates if failed()), FallbackReason.NONE)
+
+
+def _request_lengths(ends: tuple[int, ...], seqs: tuple[int, ...],
+                     prompts: tuple[int, ...]) -> list[tuple[int, int, int]]:
+    """(query_len, seq_len, prompt_len) per request.
+
+    ``ends`` are cumulative query ends.  Metadata shorter than ``seqs`` is
+    completed so that every request still gets a record: a missing end
+    repeats the previous one (query length 0) and a missing prompt length is
+    the request's sequence length.
+    """
+    last = ends[-1] if ends else 0
+    padded = list(ends[:len(seqs)]) + [last] * max(0, len(seqs) - len(ends))
+    starts = [0] + padded[:-1]
+    return [(end - start, seq, prompts[i] if i < len(prompts) else seq)
+            for i, (start, end, seq) in enumerate(zip(starts, padded, seqs))]
+
+
 def build_batch_plan(*, state_name: str, cumulative_query_ends: Sequence[int] | None,
                      seq_lens: Sequence[int] | None, prompt_lens: Sequence[int] | None,
                      num_decodes: int, num_prefills: int, config: TriangleMixConfig) -> TriangleBatchPlan:
-    """Build the step's immutable plan, reused by every selected layer."""
+    """Build the step's immutable plan, reused by every selected layer.
+
+    A batch-level reason, when there is one, overrides every request's own.
+    A step without any request still yields one placeholder request so the
+    plan carries its reason; ``batch_size`` stays 0, so stats never count it.
+    """
     started = time.perf_counter_ns()
-    ends = tuple(int(v) for v in (cumulative_query_ends or ()))
-    seqs = tuple(int(v) for v in (seq_lens or ()))
-    prompts = tuple(int(v) for v in (prompt_lens or ()))
-    batch = len(seqs)
-
-    if state_name not in PREFILL_STATES:
-        global_reason = FallbackReason.STATE_UNSUPPORTED
-    elif num_decodes:
-        global_reason = FallbackReason.MIXED_DECODE
-    elif (not ends or not seqs or not prompts or len(ends) != batch or len(prompts) != batch
-          or num_prefills != batch):
-        global_reason = FallbackReason.MISSING_METADATA
-    elif batch != 1:
-        global_reason = FallbackReason.BATCH_UNSUPPORTED
-    else:
-        global_reason = FallbackReason.NONE
-
-    requests: list[TriangleRequestPlan] = []
-    prev_end = 0
-    for i in range(batch):
-        end = ends[i] if i < len(ends) else prev_end
-        qlen = end - prev_end
-        seq = seqs[i]
-        prompt = prompts[i] if i < len(prompts) else seq
-        span, local = _request_reason(query_len=qlen, seq_len=seq, prompt_len=prompt, config=config)
-        reason = global_reason if global_reason is not FallbackReason.NONE else local
-        requests.append(TriangleRequestPlan(
-            request_index=i, q_begin=seq - qlen, q_end=seq, seq_len=seq, prompt_len=prompt,
-            span=span, eligible=reason is FallbackReason.NONE, reason=reason))
-        prev_end = end
-
+    ends, seqs, prompts = (tuple(int(v) for v in (x or ())) for x in (cumulative_query_ends, seq_lens, prompt_lens))
+    batch_reason = _batch_reason(state_name, ends, seqs, prompts, num_decodes, num_prefills)
+    requests = []
+    for index, (query_len, seq_len, prompt_len) in enumerate(_request_lengths(ends, seqs, prompts)):
+        span, own_reason = _request_reason(query_len=query_len, seq_len=seq_len, prompt_len=prompt_len,
+                                           config=config)
+        reason = own_reason if batch_reason is FallbackReason.NONE else batch_reason
+        requests.append(TriangleRequestPlan(request_index=index, q_begin=seq_len - query_len, q_end=seq_len,
+                                            seq_len=seq_len, prompt_len=prompt_len, span=span,
+                                            eligible=reason is FallbackReason.NONE, reason=reason))
     if not requests:
-        # A placeholder keeps the reason when metadata is absent; stats never
-        # count it as a user request (batch_size stays 0).
-        requests.append(TriangleRequestPlan(
-            request_index=0, q_begin=0, q_end=0, seq_len=0, prompt_len=0, span=None, eligible=False,
-            reason=global_reason if global_reason is not FallbackReason.NONE else FallbackReason.MISSING_METADATA))
-
-    return TriangleBatchPlan(
-        plan_id=next(_PLAN_IDS), state_name=state_name, batch_size=batch, requests=tuple(requests),
-        direct=len(requests) == 1 and requests[0].eligible, routing_ns=time.perf_counter_ns() - started)
+        placeholder = FallbackReason.MISSING_METADATA if batch_reason is FallbackReason.NONE else batch_reason
+        requests.append(TriangleRequestPlan(request_index=0, q_begin=0, q_end=0, seq_len=0, prompt_len=0,
+                                            span=None, eligible=False, reason=placeholder))
+    return TriangleBatchPlan(plan_id=next(_PLAN_IDS), state_name=state_name, batch_size=len(seqs),
+                             requests=tuple(requests), direct=len(requests) == 1 and requests[0].eligible,
+                             routing_ns=time.perf_counter_ns() - started)

@@ -1,9 +1,10 @@
 """Thread-safe process counters for TriangleMix routing and launches.
 
-Mirror of package/src/vllm_ascend_trianglemix/stats.py (:14-514): the same
-counter names, snapshot layout, bounded "recent" plan trace and structured
-JSON log deltas, so dashboards and log aggregators built for the reference
-read these unchanged.
+The observable contract is the reference's (package/src/vllm_ascend_trianglemix/
+stats.py): the counter names, the ``snapshot()`` layout and the structured-log
+payload of ``structured_log_if_due()`` (:373-486), so dashboards and log
+aggregators built for the reference read these unchanged.  Golden outputs
+of the reference for a fixed scenario pin it (tests/test_policy_golden.py).
 
 Counter families:
 
@@ -16,6 +17,19 @@ Counter families:
 * failures: ``runtime_error``, ``runtime_error_stage:<stage>``
 * retention drops: ``recent_layer_events_dropped``,
   ``structured_log_deltas_dropped``
+
+Design: one lock guards three parts that each own one concern --
+
+* ``_Tallies``: the flat counter maps;
+* ``_PlanTrace``: a bounded, oldest-first record per plan (the planner's view,
+  an execution tally for the plan and for each request slot, and the plan's
+  layer events up to a cap);
+* ``_LogCadence``: the structured-log schedule -- buffered deltas, the
+  request boundary they flush at, and the plans a boundary left open, whose
+  late layer events flush on their own before the next boundary.
+
+Plans are recognised by ``plan_id`` in a bounded first-seen window, so a plan
+replayed by every selected layer is counted once.
 """
 
 from __future__ import annotations
@@ -23,303 +37,332 @@ from __future__ import annotations
 import os
 import threading
 from collections import Counter, OrderedDict, deque
-from copy import deepcopy
-from typing import Any
+from typing import Any, Iterable, NamedTuple
 
 from .planning import FallbackReason, TriangleBatchPlan
 
+EVENTS_PER_PLAN = 256     # layer events kept per traced plan (later ones are counted as dropped)
+LOG_BUFFER = 8192         # structured-log deltas buffered between flushes (oldest dropped first)
+SEEN_PLAN_WINDOW = 8192   # plan ids remembered for counting each plan once
 _HOST_SCOPE = "host_enqueue_not_device_latency"
 
 
-def _route_of(plan: TriangleBatchPlan) -> str:
+class _LayerEvent(NamedTuple):
+    layer_index: int | None
+    route: str            # "direct" or "fia"
+    reason: str
+    slots: tuple[int, ...]
+    launches: int
+    saved_qk: int
+    enqueue_ns: int
+
+    def as_dict(self) -> dict[str, Any]:
+        return {"layer_index": self.layer_index, "route": self.route, "reason": self.reason,
+                "request_slots": list(self.slots), "single_launch": self.launches,
+                "estimated_saved_qk": self.saved_qk, "host_enqueue_ns": self.enqueue_ns,
+                "timing_scope": _HOST_SCOPE}
+
+    def order(self) -> tuple:
+        return (-1 if self.layer_index is None else self.layer_index, self.route, self.reason, self.slots,
+                self.enqueue_ns)
+
+
+class _Execution:
+    """What the layers of one plan (or of one request slot of it) did."""
+
+    __slots__ = ("direct", "dense", "reasons", "launches", "saved_qk", "enqueue_ns", "enqueue_max", "dropped")
+
+    def __init__(self) -> None:
+        self.direct = self.dense = self.launches = self.saved_qk = self.enqueue_ns = self.enqueue_max = 0
+        self.dropped = 0
+        self.reasons: dict[str, int] = {}
+
+    def add(self, ev: _LayerEvent) -> None:
+        if ev.route == "direct":
+            self.direct += 1
+        else:
+            self.dense += 1
+            self.reasons[ev.reason] = self.reasons.get(ev.reason, 0) + 1
+        self.launches += ev.launches
+        self.saved_qk += ev.saved_qk
+        self.enqueue_ns += ev.enqueue_ns
+        self.enqueue_max = max(self.enqueue_max, ev.enqueue_ns)
+
+    def as_dict(self) -> dict[str, Any]:
+        seen = self.direct + self.dense
+        route = {(False, False): "unobserved", (True, False): "all_direct", (False, True): "all_fia",
+                 (True, True): "mixed"}[(self.direct > 0, self.dense > 0)]
+        return {"observed_route": route, "layer_direct": self.direct, "layer_fia": self.dense,
+                "layer_hit_rate": self.direct / seen if seen else 0.0, "fallback_reasons": dict(self.reasons),
+                "single_launch": self.launches, "estimated_saved_qk": self.saved_qk,
+                "host_enqueue_ns_total": self.enqueue_ns, "host_enqueue_ns_max": self.enqueue_max,
+                "timing_scope": _HOST_SCOPE, "layer_events_dropped": self.dropped}
+
+
+def _plan_route(plan: TriangleBatchPlan) -> str:
     return "planner_eligible" if plan.direct else "planner_ineligible"
 
 
-def _empty_execution() -> dict[str, Any]:
-    return {
-        "observed_route": "unobserved",
-        "layer_direct": 0,
-        "layer_fia": 0,
-        "layer_hit_rate": 0.0,
-        "fallback_reasons": {},
-        "single_launch": 0,
-        "estimated_saved_qk": 0,
-        "host_enqueue_ns_total": 0,
-        "host_enqueue_ns_max": 0,
-        "timing_scope": _HOST_SCOPE,
-        "layer_events_dropped": 0,
-    }
+class _PlanRecord:
+    """One traced plan: its header, request summaries and execution tallies."""
+
+    def __init__(self, plan: TriangleBatchPlan, requests: Iterable) -> None:
+        self.header = {"plan_id": plan.plan_id, "state": plan.state_name, "batch_size": plan.batch_size,
+                       "route": _plan_route(plan), "reason": plan.primary_reason.value}
+        self.execution = _Execution()
+        self.events: list[_LayerEvent] = []
+        self.requests: list[tuple[dict[str, Any], _Execution]] = []
+        self.by_slot: dict[int, _Execution] = {}
+        for r in requests:
+            summary = {"slot": r.request_index, "q_begin": r.q_begin, "q_end": r.q_end, "seq_len": r.seq_len,
+                       "prompt_len": r.prompt_len, "saved_qk": r.saved_qk, "eligible": r.eligible,
+                       "reason": r.reason.value}
+            tally = _Execution()
+            self.requests.append((summary, tally))
+            self.by_slot[r.request_index] = tally
+
+    def record(self, ev: _LayerEvent) -> bool:
+        """Tally ``ev``; returns False when the event list is full and the event itself is not kept."""
+        kept = len(self.events) < EVENTS_PER_PLAN
+        if kept:
+            self.events.append(ev)
+        else:
+            self.execution.dropped += 1
+        self.execution.add(ev)
+        for slot in ev.slots:
+            tally = self.by_slot.get(slot)
+            if tally is None:
+                continue
+            if not kept:
+                tally.dropped += 1
+            tally.add(ev)
+        return kept
+
+    def as_dict(self) -> dict[str, Any]:
+        return {**self.header, "execution": self.execution.as_dict(),
+                "layer_events": [ev.as_dict() for ev in sorted(self.events, key=_LayerEvent.order)],
+                "requests": [{**summary, "execution": tally.as_dict()} for summary, tally in self.requests]}
 
 
-def _apply_event(execution: dict[str, Any], *, route: str, reason: FallbackReason, single_launch: int,
-                 estimated_saved_qk: int, host_enqueue_ns: int) -> None:
-    if route == "direct":
-        execution["layer_direct"] += 1
-    else:
-        execution["layer_fia"] += 1
-        reasons = execution["fallback_reasons"]
-        reasons[reason.value] = reasons.get(reason.value, 0) + 1
-    direct, fia = execution["layer_direct"], execution["layer_fia"]
-    execution["layer_hit_rate"] = direct / (direct + fia) if direct + fia else 0.0
-    if direct and fia:
-        execution["observed_route"] = "mixed"
-    elif direct:
-        execution["observed_route"] = "all_direct"
-    elif fia:
-        execution["observed_route"] = "all_fia"
-    execution["single_launch"] += single_launch
-    execution["estimated_saved_qk"] += estimated_saved_qk
-    execution["host_enqueue_ns_total"] += host_enqueue_ns
-    execution["host_enqueue_ns_max"] = max(execution["host_enqueue_ns_max"], host_enqueue_ns)
+class _PlanTrace:
+    """The most recent ``capacity`` plans, oldest evicted first."""
+
+    def __init__(self, capacity: int) -> None:
+        self.capacity = capacity
+        self.records: OrderedDict[int, _PlanRecord] = OrderedDict()
+
+    def resize(self, capacity: int) -> None:
+        self.capacity = capacity
+        self._evict()
+
+    def add(self, plan: TriangleBatchPlan, requests: Iterable) -> None:
+        if self.capacity:
+            self.records[plan.plan_id] = _PlanRecord(plan, requests)
+            self._evict()
+
+    def _evict(self) -> None:
+        while len(self.records) > self.capacity:
+            self.records.popitem(last=False)
+
+    def clear(self) -> None:
+        self.records.clear()
 
 
-def _event_sort_key(event: dict[str, Any]) -> tuple:
-    layer = event["layer_index"]
-    return (-1 if layer is None else layer, event["route"], event["reason"], tuple(event["request_slots"]),
-            event["host_enqueue_ns"])
+class _LogCadence:
+    """When the structured log flushes, and what it has buffered.
+
+    A flush is due once the request total reaches the next multiple of the
+    interval.  Plans counted at or past a boundary stay "open" after it: a
+    buffer holding only their (late) layer events flushes on the next poll
+    without waiting for the next boundary, reported under the last boundary.
+    """
+
+    def __init__(self) -> None:
+        self.interval = 0
+        self.next_boundary = 0
+        self.last_boundary = 0
+        self.buffer: deque[dict[str, Any]] = deque()
+        self.closing: set[int] = set()   # plans counted at or past the coming boundary
+        self.open: set[int] = set()      # plans the last boundary closed over
+
+    def restart(self, interval: int, request_total: int) -> None:
+        self.interval = interval
+        self.buffer.clear()
+        self.closing.clear()
+        self.open.clear()
+        self.last_boundary = 0
+        self.next_boundary = (request_total // interval + 1) * interval if interval else 0
+
+    def reset(self) -> None:
+        self.buffer.clear()
+        self.closing.clear()
+        self.open.clear()
+        self.next_boundary = self.interval
+        self.last_boundary = 0
+
+    def push(self, delta: dict[str, Any]) -> bool:
+        """Buffer ``delta``; returns True when the oldest buffered delta had to be dropped for it."""
+        dropped = len(self.buffer) >= LOG_BUFFER
+        if dropped:
+            self.buffer.popleft()
+        self.buffer.append(delta)
+        return dropped
+
+    def plan_counted(self, plan_id: int, request_total: int) -> None:
+        if self.next_boundary and request_total >= self.next_boundary:
+            self.closing.add(plan_id)
+
+    def take(self, request_total: int) -> tuple[int, list[dict[str, Any]]] | None:
+        """(boundary, buffered deltas) when a flush is due or a supplemental flush applies, else None."""
+        if not self.interval or not self.buffer:
+            return None
+        if request_total >= self.next_boundary:
+            boundary = request_total - request_total % self.interval
+            self.next_boundary = boundary + self.interval
+            self.last_boundary = boundary
+            self.open, self.closing = self.closing, set()
+        elif self.open and all(int(d["plan_id"]) in self.open for d in self.buffer):
+            boundary = self.last_boundary
+        else:
+            return None
+        deltas = list(self.buffer)
+        self.buffer.clear()
+        return boundary, deltas
+
+
+class _Tallies:
+    def __init__(self) -> None:
+        self.counters: Counter[str] = Counter()
+        self.reasons: Counter[str] = Counter()
+        self.direct_layers: Counter[str] = Counter()
+        self.dense_layers: Counter[str] = Counter()
+
+    def clear(self) -> None:
+        for c in (self.counters, self.reasons, self.direct_layers, self.dense_layers):
+            c.clear()
+
+    def as_dict(self) -> dict[str, Any]:
+        c = self.counters
+        total, launches = c["request_total"], c["layer_direct"]
+        return {
+            "counters": dict(c),
+            "fallback_reasons": dict(self.reasons),
+            "layers": {"direct": dict(self.direct_layers), "fia": dict(self.dense_layers)},
+            "performance": {
+                "planner_eligibility_rate": c["request_planner_eligible"] / total if total else 0.0,
+                "routing_us_per_request": c["routing_ns"] / total / 1_000 if total else 0.0,
+                "host_enqueue_us_per_launch": c["host_enqueue_ns"] / launches / 1_000 if launches else 0.0,
+                "host_enqueue_us_max": c["host_enqueue_ns_max"] / 1_000,
+                "host_enqueue_timing_scope": "host_wall_time_not_device_latency",
+            },
+        }
 
 
 class TriangleMixRuntimeStats:
-    _LAYER_EVENT_CAPACITY = 256
-    _LOG_DELTA_CAPACITY = 8192
-    _SEEN_PLAN_CAPACITY = 8192
+    """Counters, a bounded per-plan trace and the structured-log cadence of one process."""
 
     def __init__(self) -> None:
         self._lock = threading.Lock()
-        self._counters: Counter[str] = Counter()
-        self._fallback_reasons: Counter[str] = Counter()
-        self._layer_direct: Counter[str] = Counter()
-        self._layer_fia: Counter[str] = Counter()
-        self._seen_plans: OrderedDict[int, None] = OrderedDict()
-        self._recent: OrderedDict[int, dict[str, Any]] = OrderedDict()
-        self._recent_capacity = 256
-        self._log_deltas: deque[dict[str, Any]] = deque()
-        self._due_log_plan_ids: set[int] = set()
-        self._active_log_plan_ids: set[int] = set()
-        self._log_interval = 0
-        self._next_log_request = 0
-        self._last_log_boundary = 0
+        self._tallies = _Tallies()
+        self._trace = _PlanTrace(256)
+        self._log = _LogCadence()
+        self._seen: OrderedDict[int, None] = OrderedDict()
 
-    # ------------------------------------------------------------------ config
     def configure(self, recent_capacity: int, log_interval: int = 0) -> None:
+        """Set the plan-trace capacity and the structured-log interval (0 turns either off)."""
         if recent_capacity < 0 or log_interval < 0:
             raise ValueError("TriangleMix stats configuration must be non-negative")
         with self._lock:
-            self._recent_capacity = recent_capacity
-            self._trim_recent_locked()
-            if log_interval != self._log_interval:
-                self._log_interval = log_interval
-                self._log_deltas.clear()
-                self._due_log_plan_ids.clear()
-                self._active_log_plan_ids.clear()
-                self._last_log_boundary = 0
-                total = self._counters["request_total"]
-                self._next_log_request = (total // log_interval + 1) * log_interval if log_interval else 0
+            self._trace.resize(recent_capacity)
+            if log_interval != self._log.interval:
+                self._log.restart(log_interval, self._tallies.counters["request_total"])
 
-    def _trim_recent_locked(self) -> None:
-        while len(self._recent) > self._recent_capacity:
-            self._recent.popitem(last=False)
-
-    # ----------------------------------------------------------------- planner
-    def _first_sight_locked(self, plan_id: int) -> bool:
-        if plan_id in self._seen_plans:
-            return False
-        self._seen_plans[plan_id] = None
-        if len(self._seen_plans) > self._SEEN_PLAN_CAPACITY:
-            self._seen_plans.popitem(last=False)
-        return True
-
+    # ------------------------------------------------------------ recording
     def record_planner_decision(self, plan: TriangleBatchPlan) -> None:
-        """Count the deterministic planner result once per plan.
+        """Count a plan's planner result, once per plan id.
 
-        Layer outcomes are kept out of the request counters, so the exported
-        request totals do not depend on the order selected layers run in.
+        Layer outcomes never feed these request counters, so they do not
+        depend on the order the selected layers run in.  A plan built without
+        request metadata carries one placeholder request for its reason; it is
+        not a user request (``batch_size`` is 0) and is not counted.
         """
         with self._lock:
-            if not self._first_sight_locked(plan.plan_id):
+            if plan.plan_id in self._seen:
                 return
-            c = self._counters
+            self._seen[plan.plan_id] = None
+            if len(self._seen) > SEEN_PLAN_WINDOW:
+                self._seen.popitem(last=False)
+            counted = plan.requests[:plan.batch_size]
+            ineligible = [r for r in counted if not r.eligible]
+            c = self._tallies.counters
             c["routing_ns"] += plan.routing_ns
-            # The placeholder request of a metadata-less plan is not a user request.
-            requests = plan.requests[:plan.batch_size]
-            eligible = sum(1 for r in requests if r.eligible)
             c["request_total"] += plan.batch_size
-            c["request_planner_eligible"] += eligible
-            c["request_planner_ineligible"] += plan.batch_size - eligible
-            for r in requests:
-                if not r.eligible:
-                    self._fallback_reasons[r.reason.value] += 1
-            if self._log_interval:
-                self._append_delta_locked({
-                    "kind": "planner",
-                    "plan_id": plan.plan_id,
-                    "state": plan.state_name,
-                    "batch_size": plan.batch_size,
-                    "route": _route_of(plan),
-                    "reason": plan.primary_reason.value,
+            c["request_planner_eligible"] += plan.batch_size - len(ineligible)
+            c["request_planner_ineligible"] += len(ineligible)
+            self._tallies.reasons.update(r.reason.value for r in ineligible)
+            if self._log.interval:
+                self._buffer_locked({
+                    "kind": "planner", "plan_id": plan.plan_id, "state": plan.state_name,
+                    "batch_size": plan.batch_size, "route": _plan_route(plan), "reason": plan.primary_reason.value,
                     "requests": [{"slot": r.request_index, "eligible": r.eligible, "reason": r.reason.value}
-                                 for r in requests],
+                                 for r in counted],
                 })
-                if self._next_log_request and c["request_total"] >= self._next_log_request:
-                    self._due_log_plan_ids.add(plan.plan_id)
-            if self._recent_capacity:
-                entries = [{
-                    "slot": r.request_index,
-                    "q_begin": r.q_begin,
-                    "q_end": r.q_end,
-                    "seq_len": r.seq_len,
-                    "prompt_len": r.prompt_len,
-                    "saved_qk": r.saved_qk,
-                    "eligible": r.eligible,
-                    "reason": r.reason.value,
-                    "execution": _empty_execution(),
-                } for r in requests]
-                self._recent[plan.plan_id] = {
-                    "plan_id": plan.plan_id,
-                    "state": plan.state_name,
-                    "batch_size": plan.batch_size,
-                    "route": _route_of(plan),
-                    "reason": plan.primary_reason.value,
-                    "execution": _empty_execution(),
-                    "layer_events": [],
-                    "requests": entries,
-                    "_request_positions": {e["slot"]: i for i, e in enumerate(entries)},
-                }
-                self._trim_recent_locked()
+                self._log.plan_counted(plan.plan_id, c["request_total"])
+            self._trace.add(plan, counted)
 
-    def record_request_decision(self, plan: TriangleBatchPlan, *, direct: bool | None = None,
-                                reason: FallbackReason | None = None) -> None:
-        """Compatibility alias: runtime outcomes never override the planner."""
-        del direct, reason
-        self.record_planner_decision(plan)
-
-    # ------------------------------------------------------------------ layers
     def record_layer_dispatch(self, *, plan_id: int, layer_index: int | None, saved_qk: int,
                               host_enqueue_ns: int, request_index: int = 0) -> None:
+        """A selected layer ran the sparse kernel (one launch)."""
         with self._lock:
-            c = self._counters
+            c = self._tallies.counters
             c["layer_direct"] += 1
             c["single_launch"] += 1
             c["estimated_saved_qk"] += saved_qk
             c["host_enqueue_ns"] += host_enqueue_ns
             c["host_enqueue_ns_max"] = max(c["host_enqueue_ns_max"], host_enqueue_ns)
-            self._layer_direct[str(layer_index)] += 1
-            self._layer_event_locked(plan_id=plan_id, layer_index=layer_index, route="direct",
-                                     reason=FallbackReason.NONE, request_indices=(request_index,),
-                                     single_launch=1, estimated_saved_qk=saved_qk, host_enqueue_ns=host_enqueue_ns)
+            self._tallies.direct_layers[str(layer_index)] += 1
+            self._layer_event_locked(plan_id, _LayerEvent(layer_index, "direct", FallbackReason.NONE.value,
+                                                          (request_index,), 1, saved_qk, host_enqueue_ns))
 
     def record_layer_fallback(self, *, plan_id: int | None = None, layer_index: int | None,
                               reason: FallbackReason, request_indices: tuple[int, ...] = ()) -> None:
         """A selected layer that ran the dense companion kernel instead."""
         with self._lock:
-            self._counters["layer_fia"] += 1
-            self._layer_fia[str(layer_index)] += 1
-            self._counters[f"layer_fia_reason:{reason.value}"] += 1
+            c = self._tallies.counters
+            c["layer_fia"] += 1
+            c[f"layer_fia_reason:{reason.value}"] += 1
+            self._tallies.dense_layers[str(layer_index)] += 1
             if plan_id is not None:
-                self._layer_event_locked(plan_id=plan_id, layer_index=layer_index, route="fia", reason=reason,
-                                         request_indices=request_indices, single_launch=0,
-                                         estimated_saved_qk=0, host_enqueue_ns=0)
-
-    def _layer_event_locked(self, *, plan_id: int, layer_index: int | None, route: str, reason: FallbackReason,
-                            request_indices: tuple[int, ...], single_launch: int, estimated_saved_qk: int,
-                            host_enqueue_ns: int) -> None:
-        slots = sorted(set(request_indices))
-        event = {
-            "layer_index": layer_index,
-            "route": route,
-            "reason": reason.value,
-            "request_slots": list(slots),
-            "single_launch": single_launch,
-            "estimated_saved_qk": estimated_saved_qk,
-            "host_enqueue_ns": host_enqueue_ns,
-            "timing_scope": _HOST_SCOPE,
-        }
-        # The structured log is fed even when the recent trace is disabled or
-        # the plan was already evicted from it.
-        if self._log_interval and plan_id in self._seen_plans:
-            self._append_delta_locked({"kind": "layer_execution", "plan_id": plan_id, **event})
-        entry = self._recent.get(plan_id)
-        if entry is None:
-            return
-        dropped = len(entry["layer_events"]) >= self._LAYER_EVENT_CAPACITY
-        if dropped:
-            entry["execution"]["layer_events_dropped"] += 1
-            self._counters["recent_layer_events_dropped"] += 1
-        else:
-            entry["layer_events"].append(event)
-        kwargs = dict(route=route, reason=reason, single_launch=single_launch,
-                      estimated_saved_qk=estimated_saved_qk, host_enqueue_ns=host_enqueue_ns)
-        _apply_event(entry["execution"], **kwargs)
-        for slot in slots:
-            pos = entry["_request_positions"].get(slot)
-            if pos is None:
-                continue
-            request = entry["requests"][pos]
-            if dropped:
-                request["execution"]["layer_events_dropped"] += 1
-            _apply_event(request["execution"], **kwargs)
-
-    def _append_delta_locked(self, delta: dict[str, Any]) -> None:
-        if len(self._log_deltas) >= self._LOG_DELTA_CAPACITY:
-            self._log_deltas.popleft()
-            self._counters["structured_log_deltas_dropped"] += 1
-        self._log_deltas.append(delta)
+                self._layer_event_locked(plan_id, _LayerEvent(layer_index, "fia", reason.value,
+                                                              tuple(sorted(set(request_indices))), 0, 0, 0))
 
     def record_runtime_error(self, *, stage: str) -> None:
-        """Count a fail-open error (no exception text is stored)."""
+        """Count a fail-open error (no exception text is kept)."""
         with self._lock:
-            self._counters["runtime_error"] += 1
-            self._counters[f"runtime_error_stage:{stage}"] += 1
+            self._tallies.counters["runtime_error"] += 1
+            self._tallies.counters[f"runtime_error_stage:{stage}"] += 1
 
-    # --------------------------------------------------------------- snapshot
-    def _snapshot_locked(self, *, include_recent: bool) -> dict[str, Any]:
-        c = self._counters
-        total = c["request_total"]
-        direct = c["layer_direct"]
-        result: dict[str, Any] = {
-            "counters": dict(c),
-            "fallback_reasons": dict(self._fallback_reasons),
-            "layers": {"direct": dict(self._layer_direct), "fia": dict(self._layer_fia)},
-            "performance": {
-                "planner_eligibility_rate": c["request_planner_eligible"] / total if total else 0.0,
-                "routing_us_per_request": c["routing_ns"] / total / 1_000 if total else 0.0,
-                "host_enqueue_us_per_launch": c["host_enqueue_ns"] / direct / 1_000 if direct else 0.0,
-                "host_enqueue_us_max": c["host_enqueue_ns_max"] / 1_000,
-                "host_enqueue_timing_scope": "host_wall_time_not_device_latency",
-            },
-        }
-        if include_recent:
-            recent = deepcopy(list(self._recent.values()))
-            for entry in recent:
-                entry.pop("_request_positions", None)
-                entry["layer_events"].sort(key=_event_sort_key)
-            result["recent"] = recent
-        return result
+    def _layer_event_locked(self, plan_id: int, ev: _LayerEvent) -> None:
+        # The structured log gets every event of a plan it has counted, traced or not: production runs
+        # often disable the trace, and a plan can leave the trace before its last layers run.
+        if self._log.interval and plan_id in self._seen:
+            self._buffer_locked({"kind": "layer_execution", "plan_id": plan_id, **ev.as_dict()})
+        record = self._trace.records.get(plan_id)
+        if record is not None and not record.record(ev):
+            self._tallies.counters["recent_layer_events_dropped"] += 1
 
+    def _buffer_locked(self, delta: dict[str, Any]) -> None:
+        if self._log.push(delta):
+            self._tallies.counters["structured_log_deltas_dropped"] += 1
+
+    # ------------------------------------------------------------- reading
     def structured_log_if_due(self) -> dict[str, Any] | None:
-        """Worker-local counters plus incremental plan events, when due."""
+        """This worker's counters plus the plan events buffered since the last flush, when a flush applies."""
         with self._lock:
-            total = self._counters["request_total"]
-            if not self._log_interval or not self._log_deltas:
+            taken = self._log.take(self._tallies.counters["request_total"])
+            if taken is None:
                 return None
-            due = total >= self._next_log_request
-            pending = {int(d["plan_id"]) for d in self._log_deltas}
-            # Layer events of the plans that crossed the last boundary are
-            # flushed between boundaries as supplemental deltas.
-            supplemental = (not due and bool(self._active_log_plan_ids)
-                            and pending.issubset(self._active_log_plan_ids))
-            if not due and not supplemental:
-                return None
-            if due:
-                boundary = (total // self._log_interval) * self._log_interval
-                self._next_log_request = boundary + self._log_interval
-                self._last_log_boundary = boundary
-                self._active_log_plan_ids = set(self._due_log_plan_ids)
-                self._due_log_plan_ids.clear()
-            else:
-                boundary = self._last_log_boundary
-            deltas = deepcopy(list(self._log_deltas))
-            self._log_deltas.clear()
+            boundary, deltas = taken
             return {
                 "event": "trianglemix_runtime_stats",
                 "scope": "worker_local",
@@ -327,19 +370,19 @@ class TriangleMixRuntimeStats:
                 "request_boundary": boundary,
                 "delta_mode": "incremental_not_final_plan_snapshot",
                 "recent_delta": deltas,
-                "stats": self._snapshot_locked(include_recent=False),
+                "stats": self._tallies.as_dict(),
             }
 
     def snapshot(self, reset: bool = False) -> dict[str, Any]:
+        """Counters, per-layer maps, derived rates and the plan trace; ``reset`` starts every part afresh."""
         with self._lock:
-            result = self._snapshot_locked(include_recent=True)
+            result = self._tallies.as_dict()
+            result["recent"] = [record.as_dict() for record in self._trace.records.values()]
             if reset:
-                for container in (self._counters, self._fallback_reasons, self._layer_direct, self._layer_fia,
-                                   self._seen_plans, self._recent, self._log_deltas, self._due_log_plan_ids,
-                                   self._active_log_plan_ids):
-                    container.clear()
-                self._next_log_request = self._log_interval
-                self._last_log_boundary = 0
+                self._tallies.clear()
+                self._trace.clear()
+                self._seen.clear()
+                self._log.reset()
             return result
 
 

@@ -21,6 +21,7 @@ import pytest
 from trianglemix.config import resolve_plugin_config
 from trianglemix.kernel import TriangleMixConfig
 from trianglemix.planning import FallbackReason, build_batch_plan
+from trianglemix import stats as stats_module
 from trianglemix.stats import TriangleMixRuntimeStats
 
 KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
@@ -141,10 +142,14 @@ def test_plan_is_counted_once_across_layers(stats):
 
 def test_runtime_outcome_cannot_override_planner_result(stats):
     plan = plan4096()
-    stats.record_request_decision(plan, direct=False, reason=FallbackReason.STATIC_CAPABILITY)
+    stats.record_planner_decision(plan)
+    stats.record_layer_fallback(plan_id=plan.plan_id, layer_index=3, reason=FallbackReason.STATIC_CAPABILITY,
+                                request_indices=(0,))
     snap = stats.snapshot()
     assert snap["counters"]["request_planner_eligible"] == 1 and snap["fallback_reasons"] == {}
-    assert snap["recent"][0]["requests"][0]["reason"] == "none"
+    request = snap["recent"][0]["requests"][0]
+    assert request["reason"] == "none" and request["execution"]["observed_route"] == "all_fia"
+    assert snap["counters"]["layer_fia_reason:static_capability"] == 1
 
 
 def test_layer_and_host_enqueue_performance_counters(stats):
@@ -230,7 +235,7 @@ def test_per_plan_layer_event_sample_is_bounded(stats):
                                     host_enqueue_ns=10)
     snap = stats.snapshot()
     recent = snap["recent"][0]
-    assert len(recent["layer_events"]) == stats._LAYER_EVENT_CAPACITY
+    assert len(recent["layer_events"]) == stats_module.EVENTS_PER_PLAN == 256
     assert recent["execution"]["layer_direct"] == 300
     assert recent["execution"]["layer_events_dropped"] == 44
     assert recent["requests"][0]["execution"]["layer_events_dropped"] == 44
@@ -310,7 +315,7 @@ def test_boundary_plan_layers_emit_supplemental_deltas(stats):
 def test_structured_delta_capacity_and_reset(stats):
     stats.configure(0, log_interval=1)
     plan = plan4096()
-    with patch.object(TriangleMixRuntimeStats, "_LOG_DELTA_CAPACITY", 2):
+    with patch.object(stats_module, "LOG_BUFFER", 2):
         stats.record_planner_decision(plan)
         stats.record_layer_dispatch(plan_id=plan.plan_id, layer_index=3, request_index=0, saved_qk=2_000_000,
                                     host_enqueue_ns=31_000)
