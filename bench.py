@@ -560,8 +560,14 @@ def _stand_in_vllm(prompt_len: int):
         def _prepare_inputs(self, scheduler_output):
             return {"layers": self.builder.build(0, scheduler_output)}, None
 
+    class TritonAttentionBackend:
+        @staticmethod
+        def get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size, cache_dtype_str="auto"):
+            return (2, num_blocks, block_size, num_kv_heads, head_size)
+
     backend = types.SimpleNamespace(TritonAttentionMetadataBuilder=TritonAttentionMetadataBuilder,
                                     TritonAttentionImpl=TritonAttentionImpl,
+                                    TritonAttentionBackend=TritonAttentionBackend,
                                     get_tensor_model_parallel_world_size=lambda: 1)
     return backend, types.SimpleNamespace(GPUModelRunner=GPUModelRunner)
 

@@ -483,15 +483,13 @@ triangle_paged_attention_kernel(KernelParams p) {
     }
   };
 
-  // Q and K/V of iteration 0 landed; the K waves' last eight loads (K of
-  // iteration 1, not read before the next barrier) may still be in flight.
-  // Only DMA data is published here, so a bare barrier (no fence: the fence
-  // of __syncthreads would wait for every outstanding load) suffices.
-  if (dma_t == 0) {
-    wait_dma_but<S::kDmaPerWave>();
-  } else {
-    wait_dma();
-  }
+  // Q and K of iteration 0 landed; every wave's last tile share (K of
+  // iteration 1, V of iteration 0: neither is read before the barrier that
+  // opens iteration 0, where each wave waits for all of its loads) may still
+  // be in flight.  Only DMA data is published here, so a bare barrier (no
+  // fence: the fence of __syncthreads would wait for every outstanding load)
+  // suffices.
+  wait_dma_but<S::kDmaPerWave>();
   __builtin_amdgcn_s_barrier();
   // Q^T operand: lane (token n, half) holds Q[q][head][16c + 8*half .. +8].
   // Read in one asm block that waits for its own reads: the compiler cannot

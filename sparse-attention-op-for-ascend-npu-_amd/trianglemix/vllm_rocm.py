@@ -3,8 +3,11 @@
 Counterpart of the reference's vLLM-Ascend plugin
 (package/src/vllm_ascend_trianglemix/plugin.py:1-16, :778-1587, :1705-1744),
 written for vLLM v1's Triton attention backend, the ROCm backend whose paged
-KV cache ``[2, blocks, 128, 8, 128]`` is exactly the op's page layout.  Four
-methods are wrapped and nothing else is touched:
+KV cache ``[2, blocks, 128, 8, 128]`` is exactly the op's page layout.  The
+layout is read from the backend's ``get_kv_cache_shape``; a blocks-first
+cache (``[blocks, 2, ...]``) is split on its second axis and, since its pages
+are not contiguous per tensor, its layers fall back (``kv_cache_unsupported``).
+Four methods are wrapped and nothing else is touched:
 
 * ``GPUModelRunner._prepare_inputs`` publishes, for the builders that run
   inside it, the scheduler-owned final prompt lengths of the step's requests
@@ -380,11 +383,53 @@ def _missing_plan(config: TriangleMixConfig) -> TriangleBatchPlan:
                             prompt_lens=None, num_decodes=0, num_prefills=0, config=config)
 
 
-def _split_kv(kv_cache: object) -> tuple[object, object]:
+KV_FIRST = "kv_first"          # [2, blocks, 128, 8, 128]: K and V are contiguous page arrays
+BLOCKS_FIRST = "blocks_first"  # [blocks, 2, 128, 8, 128]: K and V pages interleave
+
+
+def kv_cache_layout(backend_module: object) -> str | None:
+    """The paged KV cache layout the backend allocates, read from its own shape rule.
+
+    ``TritonAttentionBackend.get_kv_cache_shape`` is asked for a cache of 3
+    blocks: the axis of length 2 that sits next to the one of length 3 tells
+    K/V-first from blocks-first.  None when the backend offers no such rule
+    or its answer fits neither layout.
+    """
+    backend = getattr(backend_module, "TritonAttentionBackend", None)
+    rule = getattr(backend, "get_kv_cache_shape", None)
+    if not callable(rule):
+        return None
+    try:
+        shape = tuple(int(x) for x in rule(3, 128, 8, 128))
+    except Exception:
+        return None
+    if len(shape) == 5 and shape[:2] == (2, 3):
+        return KV_FIRST
+    if len(shape) == 5 and shape[:2] == (3, 2):
+        return BLOCKS_FIRST
+    return None
+
+
+def _split_kv(kv_cache: object, layout: str | None) -> tuple[object, object]:
+    """(key cache, value cache) views of a layer's KV cache, or (None, None) when they cannot be found.
+
+    A blocks-first cache splits on dim 1; its K and V views step two pages
+    per block, which the op's contiguous page layout does not take, so the
+    router falls back with ``kv_cache_unsupported``.  Without a layout from
+    the backend, a 5-D cache counts as K/V-first only when that reading is
+    unambiguous (dim 0 is 2 and dim 1 is not): a 2-block cache could be
+    either and is refused.
+    """
     if isinstance(kv_cache, (tuple, list)) and len(kv_cache) == 2:
         return kv_cache[0], kv_cache[1]
     shape = tuple(getattr(kv_cache, "shape", ()))
-    if len(shape) == 5 and shape[0] == 2:
+    if len(shape) != 5:
+        return None, None
+    if layout == KV_FIRST and shape[0] == 2:
+        return kv_cache[0], kv_cache[1]
+    if layout == BLOCKS_FIRST and shape[1] == 2:
+        return kv_cache[:, 0], kv_cache[:, 1]
+    if layout is None and shape[0] == 2 and shape[1] != 2:
         return kv_cache[0], kv_cache[1]
     return None, None
 
@@ -437,6 +482,7 @@ def _wrap_builder(builder_cls: type) -> list[tuple[object, str, object]]:
 
 def _wrap_impl(impl_cls: type, backend_module: object) -> list[tuple[object, str, object]]:
     original = impl_cls.forward
+    layout = kv_cache_layout(backend_module)
 
     @functools.wraps(original)
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None, output_scale=None,
@@ -464,7 +510,7 @@ def _wrap_impl(impl_cls: type, backend_module: object) -> list[tuple[object, str
         if split is not None and split[0] is kv_cache:
             key_cache, value_cache = split[1], split[2]
         else:
-            key_cache, value_cache = _split_kv(kv_cache)
+            key_cache, value_cache = _split_kv(kv_cache, layout)
             setattr(self, _KV_SPLIT_ATTR, (kv_cache, key_cache, value_cache))
         features = LayerFeatures(
             num_heads=heads, num_kv_heads=kv_heads, head_size=size,

@@ -325,3 +325,34 @@ def test_dense_split_plan_is_the_fastest_measured(lib, geom, items):
     qs, tq, seq = geom
     need = lib.tm_dense_paged_causal_attention_workspace_size(tq, qs, seq)
     assert _items(need) == items, (geom, _items(need))
+
+
+def _row_block_tiles(tb: int, te: int, sparse_begin: int, sparse_end: int) -> int:
+    """Tiles of 32 keys a row block [tb, te) visits (csrc/trianglemix_kernel.h row_block_tiles)."""
+    last = (te - 1) // 32
+    if tb >= sparse_begin and te <= sparse_end and sparse_end > 0 and (tb - 512) // 32 > 0:
+        return 1 + last - (tb - 512) // 32 + 1  # the sink tile + the window's tiles
+    return last + 1
+
+
+def _items_at(T: int, qs: int, tq: int, seq: int, prompt: int | None) -> tuple[int, int]:
+    sparse_begin, sparse_end = (521, max(0, prompt - 128)) if prompt else (0, 0)
+    tiles = [_row_block_tiles(tb, min(tb + 32, seq), sparse_begin, sparse_end) for tb in range(qs, seq, 32)]
+    return sum(tiles), sum(-(-n // T) for n in tiles)
+
+
+def test_long_chunk_plan_skips_the_simulation_and_takes_the_largest_items(lib):
+    """A chunk with more than 4096 candidate items (total tiles / 32, the smallest split) is not simulated:
+    its tiles spread over one item per slot, clamped to 128 tiles (csrc/trianglemix_capi.cpp
+    choose_tiles_per_split) -- for any such chunk that is 128 tiles, as total / 32 slots > 4096.
+    Pinned for the dense companion's last 2048-row chunk of a 131072-token prompt (64 row blocks of
+    4033-4096 tiles).  The TriangleMix chunk at the same place has 17458 tiles (sparse rows of 18 tiles,
+    four dense-tail rows of 4096) and stays below the bound: it is simulated."""
+    qs, tq, seq = 129024, 2048, 131072
+    total, items = _items_at(128, qs, tq, seq, None)
+    assert total // 32 > 4096 and -(-total // 32) > 128  # the shortcut applies, and it clamps
+    assert _items(lib.tm_dense_paged_causal_attention_workspace_size(tq, qs, seq)) == items == 64 * 32
+    # the item count tells T apart: one step of the candidate ladder (124 tiles) splits differently
+    assert _items_at(124, qs, tq, seq, None)[1] != items
+    sparse_total, _ = _items_at(128, qs, tq, seq, 131072)
+    assert sparse_total == 17458 and sparse_total // 32 <= 4096

@@ -11,6 +11,8 @@ reference pins its longest case the same way (operator/tests/npu_v2_correctness.
   prompt's last chunk -- its first rows, the rows around ``prompt - 128``
   where sparse rows end, and the deepest dense-tail rows -- and of a middle
   chunk; tolerances as everywhere (max-abs 2e-2, mean-abs 2e-3, rel-L2 2e-2).
+* The dense companion's last chunk, whose rows at L = 131072 exceed the
+  planner's simulation bound (one 128-tile item per slot), on row subsets.
 * The exact mask identity over the WHOLE last chunk: Q = 0 weighs every
   attended key 1/|S|, and one-hot residue V rows turn each output row into
   the residue histogram of its key set (8 moduli), so one added, dropped or
@@ -68,6 +70,27 @@ def test_long_context_rows_match_oracle(gpu, L):
             assert m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS and m["relative_l2"] <= REL_L2, (L, label,
                                                                                                          r0, m)
     assert cabi.workspace_size(CHUNK, L - CHUNK, L, prompt) > cabi.WORKSPACE_COUNTER_BYTES  # dense tail split
+
+
+@pytest.mark.parametrize("L", [32768, 131072])
+def test_long_context_dense_companion_rows_match_oracle(gpu, L):
+    """The dense companion's last 2048-row chunk: at L = 131072 its 64 row blocks of ~4096 tiles exceed the
+    planner's simulation bound and split into 128-tile items (32 per row block, merged in the launch)."""
+    qs, seq = L - CHUNK, L
+    k, v, bt = make_cache(L, 750 + L // 1024, std=1.0)
+    q = make_query(CHUNK, 950 + L // 1024, std=1.0)
+    qd, kd, vd, btd = q.to(gpu), k.to(gpu), v.to(gpu), bt.to(gpu)
+    out = torch.full_like(qd, float("nan"))
+    print(f"L={L} dense chunk qs={qs} workspace={cabi.workspace_size(CHUNK, qs, seq, None)}", flush=True)
+    cabi.dense_paged_causal_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, scale=SCALE)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert torch.isfinite(got.float()).all(), L
+    for r0, r1 in ((0, 16), (1016, 1032), (CHUNK - 16, CHUNK)):
+        expected = OA.attention_torch(q[r0:r1], k, v, bt, qs + r0, seq, seq, SCALE, dense=True)
+        m = OA.error_metrics(got[r0:r1].float().numpy(), expected.float().numpy())
+        print(f"L={L} dense rows {qs + r0}..{qs + r1 - 1}: {m}", flush=True)
+        assert m["max_abs"] <= MAX_ABS and m["mean_abs"] <= MEAN_ABS and m["relative_l2"] <= REL_L2, (L, r0, m)
 
 
 def _residue_histogram(intervals, m):

@@ -46,7 +46,14 @@ class _Metadata:
         self.use_cascade = False
 
 
-def make_backend_module(*, tp=1, bad_forward=False):
+def make_backend_module(*, tp=1, bad_forward=False, kv_layout="kv_first"):
+    class TritonAttentionBackend:
+        @staticmethod
+        def get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size, cache_dtype_str="auto"):
+            if kv_layout == "kv_first":
+                return (2, num_blocks, block_size, num_kv_heads, head_size)
+            return (num_blocks, 2, block_size, num_kv_heads, head_size)
+
     class TritonAttentionMetadataBuilder:
         def __init__(self, kv_cache_spec, layer_names, vllm_config, device):
             self.vllm_config = vllm_config
@@ -80,9 +87,12 @@ def make_backend_module(*, tp=1, bad_forward=False):
                 self.vllm_calls.append(layer.layer_name)
                 return output
 
-    return types.SimpleNamespace(TritonAttentionMetadataBuilder=TritonAttentionMetadataBuilder,
-                                 TritonAttentionImpl=TritonAttentionImpl,
-                                 get_tensor_model_parallel_world_size=lambda: tp)
+    module = types.SimpleNamespace(TritonAttentionMetadataBuilder=TritonAttentionMetadataBuilder,
+                                   TritonAttentionImpl=TritonAttentionImpl,
+                                   get_tensor_model_parallel_world_size=lambda: tp)
+    if kv_layout is not None:
+        module.TritonAttentionBackend = TritonAttentionBackend
+    return module
 
 
 def make_runner_module(builder):
@@ -468,3 +478,65 @@ def test_plan_from_common_states():
     assert decode.state_name == "DecodeOnly" and not decode.direct
     empty = V.plan_from_common(types.SimpleNamespace(), cfg, None)
     assert empty.batch_size == 0 and empty.primary_reason.value == "missing_metadata"
+
+
+# ------------------------------------------------------------ KV cache layout
+def _layout_env(monkeypatch, kv_layout):
+    ops = _Ops()
+    monkeypatch.setattr(V, "OPS", V.SeamOps(direct=ops.direct, kv_write=ops.kv_write, native_ready=lambda: True))
+    runtime_stats().snapshot(reset=True)
+    runtime_stats().configure(256, 0)
+    backend = make_backend_module(kv_layout=kv_layout)
+    assert V.patch_modules(backend)
+    return types.SimpleNamespace(backend=backend, ops=ops, monkeypatch=monkeypatch)
+
+
+def test_kv_layout_comes_from_the_backend_shape_rule():
+    assert V.kv_cache_layout(make_backend_module(kv_layout="kv_first")) == V.KV_FIRST
+    assert V.kv_cache_layout(make_backend_module(kv_layout="blocks_first")) == V.BLOCKS_FIRST
+    assert V.kv_cache_layout(make_backend_module(kv_layout=None)) is None
+    odd = types.SimpleNamespace(TritonAttentionBackend=types.SimpleNamespace(get_kv_cache_shape=lambda *a: (3, 4)))
+    assert V.kv_cache_layout(odd) is None
+
+
+def _kv(layout, blocks):
+    shape = (2, blocks, 128, 8, 128) if layout == "kv_first" else (blocks, 2, 128, 8, 128)
+    kv = torch.zeros(shape, dtype=torch.bfloat16)
+    (kv[0] if layout == "kv_first" else kv[:, 0]).fill_(1.0)  # K = 1, V = 0
+    return kv
+
+
+@pytest.mark.parametrize("blocks", [2, PAGES])
+def test_kv_first_cache_splits_on_dim0_even_with_two_blocks(monkeypatch, blocks):
+    env = _layout_env(monkeypatch, "kv_first")
+    runner = _runner(env, _builder(env), prompt=8192)
+    md = _step(runner, _common(4096, 512, 4608))
+    impl = _impl(env)
+    _forward(impl, md, 7, rows=512, kv_cache=_kv("kv_first", blocks))
+    direct = [c[1] for c in env.ops.calls if c[0] == "direct"]
+    assert len(direct) == 1 and impl.vllm_calls == []
+    kc, vc = direct[0]["key_cache"], direct[0]["value_cache"]
+    assert kc.shape == (blocks, 128, 8, 128) and kc.is_contiguous() and torch.all(kc == 1) and torch.all(vc == 0)
+
+
+@pytest.mark.parametrize("blocks", [2, PAGES])
+def test_blocks_first_cache_falls_back_with_a_reason(monkeypatch, blocks):
+    env = _layout_env(monkeypatch, "blocks_first")
+    runner = _runner(env, _builder(env), prompt=8192)
+    md = _step(runner, _common(4096, 512, 4608))
+    impl = _impl(env)
+    _forward(impl, md, 7, rows=512, kv_cache=_kv("blocks_first", blocks))
+    assert not [c for c in env.ops.calls if c[0] == "direct"] and impl.vllm_calls == ["model.layers.7.self_attn.attn"]
+    assert _counters()["layer_fia_reason:kv_cache_unsupported"] == 1
+
+
+def test_two_block_cache_without_a_shape_rule_is_refused(monkeypatch):
+    assert V._split_kv(torch.zeros(2, 2, 128, 8, 128), None) == (None, None)
+    k, v = V._split_kv(torch.zeros(2, 5, 128, 8, 128), None)
+    assert k.shape == v.shape == (5, 128, 8, 128)
+    env = _layout_env(monkeypatch, None)
+    runner = _runner(env, _builder(env), prompt=8192)
+    md = _step(runner, _common(4096, 512, 4608))
+    impl = _impl(env)
+    _forward(impl, md, 7, rows=512, kv_cache=torch.zeros(2, 2, 128, 8, 128, dtype=torch.bfloat16))
+    assert _counters()["layer_fia_reason:kv_cache_unsupported"] == 1 and impl.vllm_calls
