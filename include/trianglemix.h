@@ -100,8 +100,9 @@ int64_t tm_triangle_paged_sparse_attention_workspace_size(
  * The same TriangleMix call for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
  * has no counterpart in the reference.  No call allocates: the split-KV
- * scratch (arrival counters + partials) is a static array of 32 MiB per GPU,
- * held until the process ends; a chunk that needs more is refused with
+ * scratch (arrival counters + partials) is a static array of 64 MiB per GPU
+ * (every chunk of up to 2048 rows at L <= 32768, of up to 1024 rows at
+ * L <= 65536), held until the process ends; a chunk that needs more is refused with
  * TM_ERR_WORKSPACE before any HIP call.  The device address of the array is
  * looked up once per device, with that device current -- call with the
  * stream's device current, as for any launch.  All calls in one process on
@@ -136,6 +137,19 @@ int tm_dense_paged_causal_attention(
 /* Workspace bytes for tm_dense_paged_causal_attention, or -1 if invalid. */
 int64_t tm_dense_paged_causal_attention_workspace_size(
     int64_t query_tokens, int64_t query_start, int64_t seq_len);
+
+/*
+ * The launch plan the entry points above use for one chunk geometry: the
+ * workgroup shape (*kv_parts: 4 = two query heads over KV quarters, 2 = the
+ * four heads of a GQA group over KV halves), the most tiles of 32 keys one
+ * work item takes (*tiles_per_split) and the work items per KV head
+ * (*items_per_kv_head).  dense != 0 plans the dense companion (prompt_len is
+ * then ignored).  Returns TM_OK, or TM_ERR_INVALID_ARGUMENT for attributes the
+ * entry points would refuse.  No counterpart in the reference: a diagnostic
+ * for tests and tooling (planner regression pins, bench reports).
+ */
+int tm_chunk_plan(int dense, int64_t query_tokens, int64_t query_start, int64_t seq_len, int64_t prompt_len,
+                  int32_t* kv_parts, int32_t* tiles_per_split, int64_t* items_per_kv_head);
 
 /*
  * Paged KV write, upstream of the attention: scatters one chunk's fresh K and

@@ -63,17 +63,13 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
 // four heads and a workgroup issues half the DMA and merge work per MFMA.
 // Halves run every chunk of more than 16 row blocks (16 x row blocks quarter
 // workgroups would exceed the 256 CUs, 8 x row blocks halves ones do not up
-// to 32), and chunks of at least 4 row blocks whose halves plan splits a row
-// block over KV -- for the dense companion only when the chunk also holds at
-// least kHalvesDenseMinTiles tiles per KV head.  The thresholds are measured
-// on MI355X:
-//  * unsplit chunks of up to 16 row blocks run 15-25 % faster as quarters;
-//  * split TriangleMix chunks (a prompt's last chunk, whose dense tail rows
-//    split) of 4 row blocks and more mostly run 3-16 % faster as halves, and
-//    those of 1-3 row blocks a few % faster as quarters; quarters still win
-//    when their plan fits one round of workgroups with shorter items (the
-//    iteration test in choose_plan), e.g. the last chunk of a 2048-token
-//    prompt (20.6 against 23.9 us);
+// to 32).  Below that, a TriangleMix chunk takes the shape whose simulated
+// plan is shorter (see the costs below); a dense-companion chunk of at least
+// 4 row blocks runs as halves when their plan splits a row block over KV and
+// the chunk holds at least kHalvesDenseMinTiles tiles per KV head, as
+// quarters otherwise.  Measured on MI355X:
+//  * unsplit chunks of up to 16 row blocks run 15-25 % faster as quarters
+//    (the simulation agrees: half the iterations per item);
 //  * dense-companion chunks of up to 16 row blocks, whose rows all split, run
 //    faster as halves only with enough work: over whole prefills in chunks of
 //    128-512 (L = 4096-16384) the tile bound is the fastest rule or within
@@ -83,37 +79,44 @@ constexpr int kHalvesMinRowBlocks = 17;
 constexpr int kHalvesSplitMinRowBlocks = 4;
 constexpr int64_t kHalvesDenseMinTiles = 2048;
 
-// Split-KV sizing.  A work item runs as 16 (KV quarters) or 8 (KV halves)
-// workgroups, one per CU, so each of the item's workgroup positions has
-// slots = 256 / that many CUs.  A row block of n tiles is cut into
-// ceil(n / T) near-equal items of at most T tiles; T is chosen by simulating
-// the greedy dispatch of the items (issued heaviest row block first) onto the
-// slots, an item costing a fixed start-up + merge + store cost plus its tiles,
-// and taking the T with the shortest makespan (ties: larger T, fewer
-// partials); a plan that splits anything also pays for the in-launch merge
-// (the last split of a row block reads every partial back) and, per split
-// item, for writing its fp32 partial.  Costs are in tile times: a KV-halves workgroup runs a tile
-// per part and iteration as a quarters one does, but over two parts.  The
-// halves costs are fitted to a forced-T sweep on MI355X: over nine split
-// chunks of 128-2048 rows (prompts 2869-16384) they pick the fastest measured
-// split on all nine.  The previous costs, fixed 8 and no per-split term
-// (half the quarters' fixed cost), lost 17.7 us summed over those chunks.
-// They split 1024-2048-row chunks into up to twice the items, 4-15 % slower.
+// Split-KV sizing and shape choice.  A work item runs as 16 (KV quarters) or
+// 8 (KV halves) workgroups, one per CU, so each of the item's workgroup
+// positions has slots = 256 / that many CUs.  A row block of n tiles is cut
+// into ceil(n / T) near-equal items of at most T tiles.  A plan is costed by
+// simulating the greedy dispatch of its items (issued heaviest row block
+// first) onto the slots, in loop iterations: an item costs a fixed start-up +
+// store part plus ceil(tiles / parts) iterations (a workgroup runs one tile
+// per KV part and iteration), and a plan that splits anything pays for the
+// in-launch merge -- a fixed part plus one iteration per piece of its most
+// split row block, whose last arriving workgroup reads every partial back.
+// T is the candidate with the shortest makespan (ties: larger T, fewer
+// partials).  TriangleMix chunks of up to 16 row blocks take the shape whose
+// best plan has the shorter makespan.
+//
+// The costs are fitted to a forced-(shape, T) sweep on MI355X (every plan
+// timed after a clock warm-up, in forward, reverse and forward order) of 30
+// chunks: 21 TriangleMix ones (96-2048 rows at the end of 2560-32768-token
+// prompts) and 9 dense-companion ones.  The planned plan is the fastest
+// measured on 26 of them and at most 2.3 us slower on the rest, 4.4 us
+// summed against 18.3 for the previous costs (which kept quarters to one
+// round of workgroups and charged every split item for the merge).  Quarters
+// now take the last 512-row chunk of 3584- to 12288-token prompts in up to 1.5
+// rounds: 34.5 us against 37.6 at L = 8192.
 // T is at least kMinSplitTiles (1024 keys: a split's fp32 partial of 66 KB
 // stays small next to the K/V it reads, 16 KB per 32-key tile) and at most
-// kMaxItemTiles.  Split TriangleMix chunks of at most 16 row blocks that run
-// as halves because quarters would need more than one round of workgroups
-// may go down to kFineSplitTiles (768 keys): on five such chunks (prompts
-// 2560-4992, the last 384-512 rows) that plan ran 2-4 % faster, one more
-// piece per dense-tail row while the items still fit the 32 slots.
+// kMaxItemTiles; KV-halves plans of TriangleMix chunks of at most 16 row
+// blocks may go down to kFineSplitTiles (768 keys), one more piece per
+// dense-tail row while the items still fit the slots (2-4 % faster on the
+// last 384-512 rows of 2560-4992-token prompts).
 struct PlanCosts {
   int slots;
-  int item_fixed_tiles;  // start-up, merge and store of an item
-  int merge_tiles;       // the in-launch merge of a split row block (its last split reads every partial)
-  int split_item_tiles;  // each item of a split row block
+  int parts;            // KV parts: tiles per workgroup and iteration
+  int item_fixed;       // start-up and store of an item, in iterations
+  int merge_fixed;      // the in-launch merge of a split row block, in iterations ...
+  int merge_per_piece;  // ... plus this many per piece of the most split row block
 };
-constexpr PlanCosts kQuarterCosts{16, 15, 15, 0};  // measured
-constexpr PlanCosts kHalfCosts{32, 12, 8, 1};     // fitted
+constexpr PlanCosts kQuarterCosts{16, 4, 6, 1, 1};
+constexpr PlanCosts kHalfCosts{32, 2, 5, 3, 1};
 constexpr int kMaxSlots = 32;
 static_assert(kQuarterCosts.slots <= kMaxSlots && kHalfCosts.slots <= kMaxSlots, "simulated_makespan's slot array");
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
@@ -125,33 +128,40 @@ constexpr int kSplitStep = 4;  // candidate T: kMaxItemTiles, kMaxItemTiles - 4,
 
 int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanCosts& c) {
   int64_t slot[kMaxSlots] = {};
-  int64_t split_items = 0;
+  int most_pieces = 1;
   for (const int n : row_tiles) {
     const int pieces = (n + T - 1) / T;
-    split_items += pieces > 1 ? pieces : 0;
+    most_pieces = pieces > most_pieces ? pieces : most_pieces;
     for (int i = 0; i < pieces; ++i) {
       const int size = (int)((int64_t)(i + 1) * n / pieces - (int64_t)i * n / pieces);
       int best = 0;
       for (int k = 1; k < c.slots; ++k) best = slot[k] < slot[best] ? k : best;
-      slot[best] += c.item_fixed_tiles + size;
+      slot[best] += c.item_fixed + (size + c.parts - 1) / c.parts;
     }
   }
   int64_t makespan = 0;
   for (int k = 0; k < c.slots; ++k) makespan = slot[k] > makespan ? slot[k] : makespan;
-  return makespan + (split_items > 0 ? c.merge_tiles + c.split_item_tiles * split_items : 0);
+  return makespan + (most_pieces > 1 ? c.merge_fixed + int64_t(c.merge_per_piece) * most_pieces : 0);
 }
 
-int choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c, int min_tiles = kMinSplitTiles) {
+struct SplitChoice {
+  int tiles_per_split;
+  int64_t makespan;  // in iterations; -1 when the simulation was skipped
+};
+
+SplitChoice choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c,
+                                   int min_tiles = kMinSplitTiles) {
   int64_t total = 0;
   int longest = 0;
   for (const int n : row_tiles) {
     total += n;
     longest = n > longest ? n : longest;
   }
-  if (longest <= min_tiles) return min_tiles;  // nothing to split
+  if (longest <= min_tiles) return {min_tiles, simulated_makespan(row_tiles, min_tiles, c)};  // nothing to split
   if (total / min_tiles > kMaxSimulatedItems) {
     const int64_t per_item = (total + c.slots - 1) / c.slots;
-    return (int)(per_item < min_tiles ? min_tiles : (per_item > tmx::kMaxItemTiles ? tmx::kMaxItemTiles : per_item));
+    return {(int)(per_item < min_tiles ? min_tiles : (per_item > tmx::kMaxItemTiles ? tmx::kMaxItemTiles : per_item)),
+            -1};
   }
   int best_t = tmx::kMaxItemTiles;
   int64_t best = simulated_makespan(row_tiles, best_t, c);
@@ -162,7 +172,7 @@ int choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c
       best_t = t;
     }
   }
-  return best_t;
+  return {best_t, best};
 }
 
 // The choice depends only on the chunk geometry, which repeats for every layer
@@ -181,8 +191,18 @@ struct ChunkPlan {
 
 ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
   const int num_row_blocks = (int)row_tiles.size();
-  const int t_halves = choose_tiles_per_split(row_tiles, kHalfCosts);
-  if (num_row_blocks >= kHalvesMinRowBlocks) return {2, t_halves};
+  if (num_row_blocks >= kHalvesMinRowBlocks) return {2, choose_tiles_per_split(row_tiles, kHalfCosts).tiles_per_split};
+  const SplitChoice quarters = choose_tiles_per_split(row_tiles, kQuarterCosts);
+  if (sparse) {
+    // TriangleMix: the shape whose best plan has the shorter makespan.
+    const SplitChoice halves = choose_tiles_per_split(row_tiles, kHalfCosts, kFineSplitTiles);
+    const bool use_halves = halves.makespan >= 0 && quarters.makespan >= 0 ? halves.makespan < quarters.makespan
+                                                                           : quarters.makespan < 0;
+    return use_halves ? ChunkPlan{2, halves.tiles_per_split} : ChunkPlan{4, quarters.tiles_per_split};
+  }
+  // Dense companion: halves when their plan splits a row block and the chunk
+  // holds at least kHalvesDenseMinTiles tiles per KV head (the measured rule).
+  const int t_halves = choose_tiles_per_split(row_tiles, kHalfCosts).tiles_per_split;
   if (num_row_blocks >= kHalvesSplitMinRowBlocks) {
     int64_t total = 0;
     bool split = false;
@@ -190,31 +210,9 @@ ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
       total += n;
       split = split || n > t_halves;
     }
-    if (split && !sparse && total >= kHalvesDenseMinTiles) return {2, t_halves};
-    if (split && sparse) {
-      // Quarters keep a split TriangleMix chunk when their plan fits one round
-      // of workgroups and its longest item needs fewer loop iterations (4
-      // tiles each) than the halves plan's (2 tiles each) -- or as many
-      // without any split, which saves the merge.
-      const int t_quarters = choose_tiles_per_split(row_tiles, kQuarterCosts);
-      int64_t q_items = 0;
-      int q_iters = 0, h_iters = 0;
-      bool q_split = false;
-      for (const int n : row_tiles) {
-        const int qp = (n + t_quarters - 1) / t_quarters;
-        const int hp = (n + t_halves - 1) / t_halves;
-        q_items += qp;
-        q_split = q_split || qp > 1;
-        q_iters = std::max(q_iters, ((n + qp - 1) / qp + 3) / 4);
-        h_iters = std::max(h_iters, ((n + hp - 1) / hp + 1) / 2);
-      }
-      if (q_items <= kQuarterCosts.slots && (q_iters < h_iters || (q_iters == h_iters && !q_split))) {
-        return {4, t_quarters};
-      }
-      return {2, choose_tiles_per_split(row_tiles, kHalfCosts, kFineSplitTiles)};
-    }
+    if (split && total >= kHalvesDenseMinTiles) return {2, t_halves};
   }
-  return {4, choose_tiles_per_split(row_tiles, kQuarterCosts)};
+  return {4, quarters.tiles_per_split};
 }
 
 ChunkPlan cached_plan(const PlanKey& key) {
@@ -434,6 +432,23 @@ int64_t tm_dense_paged_causal_attention_workspace_size(int64_t query_tokens, int
   g_last_error[0] = '\0';
   if (check_attributes(query_tokens, query_start, seq_len, seq_len, false) != TM_OK) return -1;
   return make_geometry(false, query_tokens, query_start, seq_len, seq_len).workspace_bytes;
+}
+
+int tm_chunk_plan(int dense, int64_t query_tokens, int64_t query_start, int64_t seq_len, int64_t prompt_len,
+                  int32_t* kv_parts, int32_t* tiles_per_split, int64_t* items_per_kv_head) {
+  g_last_error[0] = '\0';
+  if (kv_parts == nullptr || tiles_per_split == nullptr || items_per_kv_head == nullptr) {
+    return fail(TM_ERR_INVALID_ARGUMENT, "tm_chunk_plan: null output pointer");
+  }
+  const bool sparse = dense == 0;
+  const int64_t prompt = sparse ? prompt_len : seq_len;
+  const int status = check_attributes(query_tokens, query_start, seq_len, prompt, sparse);
+  if (status != TM_OK) return status;
+  const Geometry g = make_geometry(sparse, query_tokens, query_start, seq_len, prompt);
+  *kv_parts = g.kv_parts;
+  *tiles_per_split = g.tiles_per_split;
+  *items_per_kv_head = g.items_per_head;
+  return TM_OK;
 }
 
 int tm_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,

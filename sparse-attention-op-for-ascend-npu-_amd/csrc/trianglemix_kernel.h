@@ -38,9 +38,10 @@ constexpr int64_t kPartialBytes = kPartialFloats * 4;
 constexpr int64_t kCounterBytes = 65536;
 constexpr int kMaxSplitRowBlocks = int(kCounterBytes / 4 / (kKvHeads * 2));  // 1024
 // Split-KV scratch held per GPU for the no-allocation entry point (counter
-// block + partials): enough for the TriangleMix chunks of up to 2048 rows
-// at L <= 16384 that split their dense-tail rows.
-constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
+// block + partials): enough for every TriangleMix chunk of up to 2048 rows
+// at L <= 32768 and of up to 1024 rows at L <= 65536 (their splits need at
+// most 50 MB).
+constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
 // Largest number of tiles one work item may hold: the kernel keeps the item's
 // page numbers in two 64-lane registers.  Longer rows are split.
 constexpr int kMaxItemTiles = 128;

@@ -8,6 +8,8 @@ current stream of the query's device).
 
 from __future__ import annotations
 
+import ctypes
+
 from .native import load_hip_library
 
 TM_OK = 0
@@ -46,6 +48,18 @@ def workspace_size(query_tokens: int, query_start: int, seq_len: int, prompt_len
     if n < 0:
         raise TriangleMixError(TM_ERR_INVALID_ARGUMENT, lib.tm_last_error().decode())
     return int(n)
+
+
+def chunk_plan(query_tokens: int, query_start: int, seq_len: int, prompt_len: int | None) -> tuple[int, int, int]:
+    """(KV parts, tiles per work item, work items per KV head) the launch uses for this chunk geometry;
+    ``prompt_len`` None plans the dense companion."""
+    lib = load_hip_library()
+    parts, tiles, items = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    dense = prompt_len is None
+    status = lib.tm_chunk_plan(int(dense), query_tokens, query_start, seq_len, 0 if dense else prompt_len,
+                               ctypes.byref(parts), ctypes.byref(tiles), ctypes.byref(items))
+    _check(status)
+    return parts.value, tiles.value, items.value
 
 
 # Split-KV workspace per (device, stream): the first WORKSPACE_COUNTER_BYTES

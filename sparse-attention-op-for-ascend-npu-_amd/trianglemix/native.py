@@ -79,6 +79,9 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_float, vp, i64, vp]
     lib.tm_dense_paged_causal_attention_workspace_size.restype = i64
     lib.tm_dense_paged_causal_attention_workspace_size.argtypes = [i64, i64, i64]
+    lib.tm_chunk_plan.restype = ctypes.c_int
+    lib.tm_chunk_plan.argtypes = [ctypes.c_int, i64, i64, i64, i64, ctypes.POINTER(ctypes.c_int32),
+                                  ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64)]
     lib.tm_reshape_and_cache.restype = ctypes.c_int
     lib.tm_reshape_and_cache.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, vp]
     del i32p

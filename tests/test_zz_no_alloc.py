@@ -42,9 +42,9 @@ def test_noalloc_matches_workspace_entry_point(gpu):
 
 
 def test_noalloc_refuses_oversized_chunk(gpu):
-    # a dense 2048-row chunk ending at L = 131072 splits every row: far more scratch than 32 MiB
+    # a dense 2048-row chunk ending at L = 131072 splits every row: far more scratch than 64 MiB
     qs, tq = 131072 - 2048, 2048
-    assert cabi.workspace_size(tq, qs, 131072, 131072) > 32 << 20
+    assert cabi.workspace_size(tq, qs, 131072, 131072) > 64 << 20
     q = torch.empty((tq, 32, 128), dtype=torch.bfloat16, device=gpu)
     kv = torch.empty((1, 128, 8, 128), dtype=torch.bfloat16, device=gpu)
     bt = torch.zeros((1, 1024), dtype=torch.int32, device=gpu)
