@@ -7,6 +7,8 @@ Outputs (next to the Python package, git-ignored, shipped with the tree):
   linked to the library above through ``$ORIGIN``
 
 Usage: ``python build.py [--hip-only]``.  Each call recompiles.
+``python build.py --phase-clocks`` builds the diagnostic phase-clock library
+``trianglemix/libtrianglemix_phase_clocks.so`` instead (see trianglemix/phase_clocks.py).
 """
 
 from __future__ import annotations
@@ -27,6 +29,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 
 HIP_LIB = PKG / "libtrianglemix.so"
+PHASE_CLOCK_LIB = PKG / "libtrianglemix_phase_clocks.so"  # diagnostic build (--phase-clocks), not loaded by the op
 TORCH_LIB = PKG / "_trianglemix_torch.so"
 
 # Disable packed fp32 VALU ops in device code: some of their forms have given
@@ -65,14 +68,17 @@ def _atomic_replace(tmp: Path, dst: Path) -> None:
     os.replace(tmp, dst)
 
 
-def build_hip_library() -> Path:
+def build_hip_library(phase_clocks: bool = False) -> Path:
+    """The kernels + C ABI; ``phase_clocks`` builds the diagnostic variant that records per-wave phase clocks
+    (trianglemix/phase_clocks.py reads them) into its own file."""
     hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
-    tmp = HIP_LIB.with_suffix(".so.tmp")
-    _run([hipcc, *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
+    dst = PHASE_CLOCK_LIB if phase_clocks else HIP_LIB
+    tmp = dst.with_suffix(".so.tmp")
+    _run([hipcc, *HIP_FLAGS, *(["-DTRIANGLEMIX_PHASE_CLOCKS"] if phase_clocks else []), "-shared", f"-I{INCLUDE}",
           str(CSRC / "trianglemix_kernel.hip"), str(CSRC / "trianglemix_cache.hip"), str(CSRC / "trianglemix_capi.cpp"),
           "-o", str(tmp)])
-    _atomic_replace(tmp, HIP_LIB)
-    return HIP_LIB
+    _atomic_replace(tmp, dst)
+    return dst
 
 
 def build_torch_adapter() -> Path:
@@ -107,7 +113,12 @@ def build_all(hip_only: bool = False) -> list[Path]:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--hip-only", action="store_true")
+    ap.add_argument("--phase-clocks", action="store_true",
+                    help="build only the diagnostic phase-clock library (libtrianglemix_phase_clocks.so)")
     args = ap.parse_args()
+    if args.phase_clocks:
+        print(f"built {build_hip_library(phase_clocks=True)}")
+        return 0
     for p in build_all(args.hip_only):
         print(f"built {p}")
     return 0

@@ -107,6 +107,27 @@ typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
+
+// Phase clocks (diagnostic builds only, -DTRIANGLEMIX_PHASE_CLOCKS): lane 0 of
+// every wave stores the 100 MHz s_memrealtime clock at the phases listed in
+// trianglemix/phase_clocks.py, one 64-bit slot per (workgroup, wave, phase),
+// for grids of up to kPhaseClockWorkgroups workgroups.  The product library
+// is built without them.
+#ifdef TRIANGLEMIX_PHASE_CLOCKS
+constexpr int kPhaseClockWorkgroups = 4096;
+constexpr int kPhaseClockSlots = 32;
+__device__ unsigned long long phase_clocks[kPhaseClockWorkgroups * kWaves * kPhaseClockSlots];
+#define TM_PHASE(slot)                                                                                   \
+  do {                                                                                                   \
+    const unsigned long long tm_clock_ = __builtin_amdgcn_s_memrealtime();                               \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < kPhaseClockWorkgroups)                                   \
+      phase_clocks[(blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPhaseClockSlots + (slot)] = tm_clock_; \
+  } while (0)
+#else
+#define TM_PHASE(slot) \
+  do {                 \
+  } while (0)
+#endif
 constexpr int kRowBytes = kHeadDim * 2;          // 256 B: one key row
 constexpr int kTileBytes = kKvTile * kRowBytes;  // 8 KB: K or V of one tile
 constexpr int kDmaPerTile = kTileBytes / 1024;   // 1 KB (4 key rows) per DMA instruction
@@ -288,6 +309,7 @@ triangle_paged_attention_kernel(KernelParams p) {
 
   const int sparse_begin = kSparse ? p.sparse_begin : 0;
   const int sparse_end = kSparse ? p.sparse_end : 0;
+  TM_PHASE(0);
 
   const int kvh = blockIdx.x % kKvHeads;
   const int hp = (blockIdx.x / kKvHeads) % S::kWgPerKvHead;
@@ -402,6 +424,10 @@ triangle_paged_attention_kernel(KernelParams p) {
   const unsigned row_hi = lane_row(64 + lane, phys_hi);
   const int bytes_lo = lane_bytes(lane);
   const int bytes_hi = lane_bytes(64 + lane);
+#ifdef TRIANGLEMIX_PHASE_CLOCKS
+  asm volatile("" ::"v"(row_lo), "v"(row_hi));  // the block-table loads have landed
+#endif
+  TM_PHASE(1);
   // Buffer resource of tensor t (0 = K, 1 = V) of tile ti: the tile's key rows
   // of this KV head, range cut at seq_len; a tile past the item's end gets an
   // empty range (its loads return zeros).
@@ -491,6 +517,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   // suffices.
   wait_dma_but<S::kDmaPerWave>();
   __builtin_amdgcn_s_barrier();
+  TM_PHASE(2);
   // Q^T operand: lane (token n, half) holds Q[q][head][16c + 8*half .. +8].
   // Read in one asm block that waits for its own reads: the compiler cannot
   // tell q_lds from the K slot the K waves' last DMA still writes, and would
@@ -536,6 +563,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   // O and the row sum are still zero: the first tile's max becomes the state
   // directly (the first update then rescales nothing).
   m_run = m_tile;
+  TM_PHASE(3);
 
   // Iteration it (this wave's tile ti = 4*it + kq): state update with tile
   // ti's row max, then [QK^T of tile ti+4 (K slot kr) || exponentials of tile
@@ -546,6 +574,7 @@ triangle_paged_attention_kernel(KernelParams p) {
                        char* vw) {
     wait_dma();
     __syncthreads();  // DMA issued one iteration ago landed; slots kw / vw are no longer read
+    if (it < 8) TM_PHASE(4 + it);
     const int ti = P * it + kq;
     // Ragged last iteration: the parts without a tile idle; nothing is
     // left to prefetch in the last iteration.
@@ -625,6 +654,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     if (it + 1 < num_iters) iteration(it + 1, s_b, s_a, k_lds0, v_lds1, k_lds1, v_lds0);
   }
 
+  TM_PHASE(12);
   // ---- merge the P KV parts through LDS ----
   // Part kq keeps the O = 4 / P d-blocks kq * O .. kq * O + O - 1 and hands
   // its other 4 - O d-blocks to their owners.  The given-block index gi (0 ..
@@ -729,8 +759,10 @@ triangle_paged_attention_kernel(KernelParams p) {
       }
     }
   };
+  TM_PHASE(13);
   if (nsplit == 1) {
     store_rows(kept, l_run);
+    TM_PHASE(14);
     return;
   }
 
@@ -777,6 +809,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     }
   }
   wait_dma();  // this wave's partial stores completed (vmcnt also counts stores)
+  TM_PHASE(16);
   __syncthreads();
   unsigned* ctr = p.counters + ((size_t)kvh * p.num_row_blocks + rb) * S::kWgPerKvHead + hp;
   if (tid == 0) {
@@ -784,6 +817,7 @@ triangle_paged_attention_kernel(KernelParams p) {
                    (unsigned)(nsplit - 1));
   }
   __syncthreads();
+  TM_PHASE(17);
   if (!s_last) return;
   // Leave the counter zero for the next launch (every split has arrived).
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -837,8 +871,11 @@ triangle_paged_attention_kernel(KernelParams p) {
       }
     }
     mt = mb;
+    if (s0 == 0) TM_PHASE(18);
   }
+  TM_PHASE(19);
   store_rows(acc, lt);
+  TM_PHASE(15);
 }
 
 template <bool kSparse, int P>
@@ -879,5 +916,23 @@ hipError_t noalloc_scratch(void** ptr) {
   *ptr = addresses[device];
   return hipSuccess;
 }
+
+#ifdef TRIANGLEMIX_PHASE_CLOCKS
+// Diagnostic exports of the phase-clock build: copy the clock slots to the
+// host, or clear them (before the launch to be read).
+extern "C" int tm_phase_clocks_read(void* host, int64_t bytes) {
+  if (bytes < 0 || bytes > (int64_t)sizeof(phase_clocks)) return (int)hipErrorInvalidValue;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(phase_clocks), (size_t)bytes, 0, hipMemcpyDeviceToHost);
+}
+
+extern "C" int tm_phase_clocks_clear(void) {
+  void* address = nullptr;
+  hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(phase_clocks));
+  if (err != hipSuccess) return (int)err;
+  err = hipMemset(address, 0, sizeof(phase_clocks));
+  if (err != hipSuccess) return (int)err;
+  return (int)hipDeviceSynchronize();
+}
+#endif
 
 }  // namespace tmx

@@ -73,6 +73,15 @@ def test_header_functions_are_exported(lib):
         assert getattr(raw, name) is not None, name
 
 
+def test_product_library_has_no_phase_clocks():
+    """The phase-clock instrumentation is compiled only into the diagnostic build."""
+    raw = ctypes.CDLL(str(native.HIP_LIBRARY))
+    assert not hasattr(raw, "tm_phase_clocks_read") and not hasattr(raw, "tm_phase_clocks_clear")
+    from trianglemix import phase_clocks
+    assert phase_clocks.library_path().name == "libtrianglemix_phase_clocks.so"
+    assert phase_clocks.library_path() != native.HIP_LIBRARY
+
+
 def test_abi_version_and_status_strings(lib):
     m = re.search(r"#define\s+TM_ABI_VERSION\s+(\d+)", HEADER.read_text())
     assert lib.tm_abi_version() == int(m.group(1)) == native.ABI_VERSION
