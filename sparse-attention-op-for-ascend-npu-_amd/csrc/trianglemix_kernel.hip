@@ -38,7 +38,10 @@
 // MFMAs of its tile of iteration i+1 interleaved with the exponentials of its
 // tile of iteration i, then the PV MFMAs of tile i interleaved with the mask
 // and row max of tile i+1 (the interleave is fixed in program order with
-// scheduling barriers).  LDS holds two K slots and two V slots, each with the
+// scheduling barriers); the item's last iteration has no tile i+1 and runs
+// only the exponentials and PV of its tile, after which each wave hands its
+// share of the KV-part merge to LDS slots that iteration no longer reads
+// without waiting for the others.  LDS holds two K slots and two V slots, each with the
 // P tiles (one per part) of one iteration, plus the workgroup's Q (DMA'd
 // once, read into registers in the prologue); the DMA of K for iteration
 // i+2 (waves 0-3) and of V for iteration i+1 (waves 4-7) is spread over the
@@ -162,11 +165,12 @@ static_assert(kDmaPerTile == 8, "a tile is eight 1 KB DMA instructions, one per 
 // it before a barrier that publishes DMA'd tiles to the other waves -- the
 // barrier alone does not order the DMA's LDS writes.
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-// All but the last N (< 16) vector-memory operations of this wave have landed.
+// All but the last N (< 64) vector-memory operations of this wave have landed
+// (vmcnt bits 3:0 and 15:14 of the gfx9 s_waitcnt immediate).
 template <int N>
 __device__ __forceinline__ void wait_dma_but() {
-  static_assert(N >= 0 && N < 16, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
 __device__ __forceinline__ int k_slot(int row, int chunk) { return chunk ^ (row & 15); }
@@ -247,6 +251,15 @@ __device__ __forceinline__ bf16x8_t v_operand(const char* vt, const int* v_off, 
   __builtin_memcpy(&a, lohi, sizeof(a));
   return a;
 }
+
+// The i-th exponential a full iteration adds to the row sum: block 1 step k
+// adds element k and, on even k, 8 + k/2; block 2 adds 12-15.
+__device__ __forceinline__ constexpr int sum_order(int i) {
+  return i < 12 ? (i % 3 == 1 ? 8 + i / 3 : i - (i + 1) / 3) : i;
+}
+static_assert(sum_order(0) == 0 && sum_order(1) == 8 && sum_order(2) == 1 && sum_order(4) == 9 &&
+                  sum_order(10) == 11 && sum_order(11) == 7 && sum_order(12) == 12,
+              "block 1 adds 0, 8, 1, 2, 9, 3, ..., 7");
 
 // How many MFMA steps ahead of their use the LDS operand reads are issued.
 constexpr int kReadAhead = 3;
@@ -649,9 +662,66 @@ triangle_paged_attention_kernel(KernelParams p) {
     l_run += rsum;
     m_tile = half_max(tmax) * c2;
   };
-  for (int it = 0; it < num_iters; it += 2) {
+  // The item's last iteration: no tile follows, so there is no QK^T, no
+  // prefetch and no row max of a next tile -- only this tile's exponentials
+  // and its PV.  Exponentials 0-7 (pb[0]) run before the PV steps, 8-15 two
+  // per step in steps 0-3 (pb[1] is first used at step 4), and the row sum
+  // adds them in steps 4-7 in the order the full iteration adds them, so both
+  // kinds of iteration sum a tile alike.
+  auto last_iteration = [&](int it, const f32x16_t& s_cur, const char* vr) {
+    wait_dma();
+    __syncthreads();  // V of this iteration landed
+    if (it < 8) TM_PHASE(4 + it);
+    const int ti = P * it + kq;
+    if (ti >= num_tiles) return;
+    const float shift = softmax_update(m_tile, m_run, l_run, o_acc);
+    bf16x8_t va[8];
+#pragma unroll
+    for (int k = 0; k < kReadAhead; ++k) va[k] = v_operand(vr, v_off, k);
+    float px[16];
+    auto expo = [&](int e) { px[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[e], c2, -shift)); };
+#pragma unroll
+    for (int e = 0; e < 8; ++e) expo(e);
+    bf16x8_t pb[2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pb[0][e] = (__bf16)px[e];
+    __builtin_amdgcn_sched_barrier(0);
+    float rsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k + kReadAhead < 8) va[k + kReadAhead] = v_operand(vr, v_off, k + kReadAhead);
+      if (k < 4) {
+        expo(8 + 2 * k);
+        expo(9 + 2 * k);
+        if (k == 3) {
+#pragma unroll
+          for (int e = 8; e < 16; ++e) pb[1][e - 8] = (__bf16)px[e];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rsum += px[sum_order(4 * (k - 4) + j)];
+      }
+      o_acc[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[k], pb[k >> 2], o_acc[k & 3], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l_run += rsum;
+  };
+  // Pairs of full iterations (slots alternate, so the loop is unrolled by
+  // two), at most one more full iteration, then the last.  The last iteration
+  // has one call site (its slots chosen by parity): with one per parity the
+  // compiler copies the O accumulators between the two paths.
+  int it = 0;
+  for (; it + 2 < num_iters; it += 2) {
     iteration(it, s_a, s_b, k_lds1, v_lds0, k_lds0, v_lds1);
-    if (it + 1 < num_iters) iteration(it + 1, s_b, s_a, k_lds0, v_lds1, k_lds1, v_lds0);
+    iteration(it + 1, s_b, s_a, k_lds0, v_lds1, k_lds1, v_lds0);
+  }
+  if (it + 1 < num_iters) {
+    iteration(it, s_a, s_b, k_lds1, v_lds0, k_lds0, v_lds1);
+    ++it;
+  }
+  if (it < num_iters) {
+    const bool odd = (it & 1) != 0;
+    last_iteration(it, odd ? s_b : s_a, odd ? v_lds1 : v_lds0);
   }
 
   TM_PHASE(12);
@@ -660,26 +730,35 @@ triangle_paged_attention_kernel(KernelParams p) {
   // its other 4 - O d-blocks to their owners.  The given-block index gi (0 ..
   // 3 - O among the blocks a part gives away) and the giving wave w = hl * P +
   // part select a 4 KB stretch xo(gi, w) = [v/4][lane][4] (16-byte accesses,
-  // one 1 KB stretch per instruction): for P = 4 the stretches of gi = 0, 1, 2
-  // fill k_lds0, k_lds1, v_lds0 and xm / xl [hl][part][lane] live in v_lds1;
-  // for P = 2 gi = 0 fills q_lds, gi = 1 fills k_lds0 (waves 0-3) and k_lds1
-  // (waves 4-7), and xm / xl live in v_lds0.  kq is wave-uniform, so the
-  // per-block branches are scalar; both barriers stay outside them.
-  wait_dma();
-  __syncthreads();  // all compute and every (empty) prefetch done; the slots are free
+  // one 1 KB stretch per instruction).  The item's last iteration reads only
+  // its V slot: the K slots, the other V slot (v_free) and q_lds are idle from
+  // the barrier that opens it (no DMA is in flight after that barrier), so each
+  // wave writes its blocks as soon as its own last PV is done, with no barrier
+  // in between.  For P = 4 the stretches of gi = 0, 1, 2 fill k_lds0, k_lds1,
+  // v_free and xm / xl [hl][part][lane] live in q_lds; for P = 2 gi = 0 fills
+  // q_lds, gi = 1 fills k_lds0 (waves 0-3) and k_lds1 (waves 4-7), and xm / xl
+  // live in v_free.  kq is wave-uniform, so the per-block branches are scalar;
+  // the barrier stays outside them.
+  if (num_iters == 0) {  // no iteration ran: the prologue DMA may still be landing
+    wait_dma();
+    __syncthreads();
+  }
+  char* v_free = (num_iters & 1) ? v_lds1 : v_lds0;  // the last iteration read v_lds((num_iters - 1) % 2)
   constexpr int O = S::kOwned;
   static_assert(P != 4 || H * P * 4 * 64 * 16 == S::kSlotBytes, "P = 4: one given block of all waves fills a slot");
+  static_assert(P != 4 || 2 * H * P * 64 * 4 <= H * kRowBlock * kRowBytes, "P = 4: xm / xl fit in q_lds");
   static_assert(P != 2 || (H * P * 4 * 64 * 16 == H * kRowBlock * kRowBytes && 4 * 4 * 64 * 16 == S::kSlotBytes),
                 "P = 2: one given block of all waves fills q_lds, half of one fills a slot");
+  static_assert(P != 2 || 2 * H * P * 64 * 4 <= S::kSlotBytes, "P = 2: xm / xl fit in a slot");
   auto xo = [&](int gi, int w) -> f32x4_t* {
     if constexpr (P == 4) {
-      return reinterpret_cast<f32x4_t*>(gi == 0 ? k_lds0 : (gi == 1 ? k_lds1 : v_lds0)) + w * 4 * 64;
+      return reinterpret_cast<f32x4_t*>(gi == 0 ? k_lds0 : (gi == 1 ? k_lds1 : v_free)) + w * 4 * 64;
     } else {
       if (gi == 0) return reinterpret_cast<f32x4_t*>(q_lds) + w * 4 * 64;
       return reinterpret_cast<f32x4_t*>(w < 4 ? k_lds0 : k_lds1) + (w & 3) * 4 * 64;
     }
   };
-  float* xm = reinterpret_cast<float*>(P == 4 ? v_lds1 : v_lds0);
+  float* xm = reinterpret_cast<float*>(P == 4 ? q_lds : v_free);
   float* xl = xm + H * P * 64;
   const int self = hl * P + kq;
   // Index of d-block m among the blocks part r gives away (m is not r's).
