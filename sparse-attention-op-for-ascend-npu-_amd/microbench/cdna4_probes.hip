@@ -12,13 +12,24 @@
 //  3. MFMA issue (v_mfma_f32_32x32x16_bf16, two independent accumulators)
 //     with n independent VALU instructions (v_exp_f32 or v_fma_f32) after
 //     each MFMA, at 1 and 2 waves per SIMD: time per MFMA per SIMD.
+//  4. The attention loop body (one 32-key tile per wave and iteration: K
+//     reads, the QK^T chain, exponentials, row sum and max, V transposed
+//     reads, PV into four accumulators, 1 KB of LDS DMA per MFMA step and a
+//     barrier per iteration -- the kernel's KV-quarter shape, 8 waves per CU)
+//     and the same work as 4 waves of two heads each (every K/V read feeds
+//     two MFMAs, one wave per SIMD).  K/V come from an L2-resident buffer of
+//     zeros or of random bf16 values; each row gives the time per iteration,
+//     the shader clock over the launch (s_memtime against the 100 MHz
+//     s_memrealtime) and the cycles per iteration.
 //
 // Build and run: python -m trianglemix.microbench  (or hipcc --offload-arch=gfx950 -O3 this file).
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 
 namespace {
 
@@ -180,6 +191,141 @@ __global__ void __launch_bounds__(512) mfma_valu(float* sink, int rounds) {
   sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// ---- 4. The attention loop body, in the kernel's shape (H2 = 1) and with two heads per wave (H2 = 2).
+__device__ __forceinline__ bf16x8 v_pair(const char* vt, const int* v_off, int k) {  // the V^T operand
+  const char* a0 = vt + 16 * (k >> 2) * 256 + v_off[k & 3];
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a0 + 2048));
+  const i16x4 both[2] = {lo, hi};
+  bf16x8 a;
+  __builtin_memcpy(&a, both, sizeof(a));
+  return a;
+}
+
+template <int H2>
+__global__ void __launch_bounds__(512 / H2) loop_body(const char* src, float* sink, int iters,
+                                                      unsigned long long* clocks) {
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  constexpr int kWavesPerCu = 8 / H2;
+  constexpr int kDma = 64 / kWavesPerCu;  // 1 KB DMA instructions per wave and iteration: 64 KB per CU
+  __shared__ __attribute__((aligned(1024))) char k0[32768];
+  __shared__ __attribute__((aligned(1024))) char k1[32768];
+  __shared__ __attribute__((aligned(1024))) char v0[32768];
+  __shared__ __attribute__((aligned(1024))) char v1[32768];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int part = H2 == 1 ? wave / 2 : wave;  // four KV parts, 8 KB tiles
+  const int n = lane & 31;
+  // the kernel's swizzled read offsets (K: chunk c of row r in slot c ^ (r % 16); V: c ^ 4 (r % 4))
+  int k_off[8], v_off[4];
+  for (int c = 0; c < 8; ++c) k_off[c] = part * 8192 + n * 256 + 16 * ((2 * c + (lane >> 5)) ^ (n & 15));
+  const int tr_key = 4 * (lane >> 5) + ((lane & 15) >> 2);
+  for (int m = 0; m < 4; ++m) {
+    const int d = 32 * m + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    v_off[m] = part * 8192 + tr_key * 256 + 16 * ((d >> 3) ^ ((tr_key & 3) << 2)) + 2 * (d & 7);
+  }
+  bf16x8 qreg[H2][8];
+  for (int h = 0; h < H2; ++h)
+    for (int c = 0; c < 8; ++c)
+      for (int e = 0; e < 8; ++e) qreg[h][c][e] = (__bf16)((float)(((lane * 37 + h * 11 + c * 5 + e * 3) % 17) - 8) * 0.11f);
+  f32x16 o_acc[H2][4], s_a[H2], s_b[H2];
+  float m_run[H2], l_run[H2], m_tile[H2];
+  for (int h = 0; h < H2; ++h) {
+    for (int m = 0; m < 4; ++m) o_acc[h][m] = f32x16{};
+    s_a[h] = f32x16{};
+    s_b[h] = f32x16{};
+    m_run[h] = l_run[h] = m_tile[h] = 0.0f;
+  }
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, kSourceBytes, 0x00020000);
+  const float c2 = 0.127f;
+  // one iteration: state update, [QK^T of the next tile || exponentials of this tile, DMA into kw], then
+  // [PV of this tile || last exponentials and the next tile's row max]
+  auto iteration = [&](int it, f32x16* s_cur, f32x16* s_nxt, const char* kr, const char* vr, char* kw) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    float shift[H2], rsum[H2], px[H2][16], tmax[H2];
+    for (int h = 0; h < H2; ++h) {
+      if (__any(m_tile[h] > m_run[h] + 8.0f)) {
+        const float a = __builtin_amdgcn_exp2f(m_run[h] - m_tile[h]);
+        l_run[h] *= a;
+        for (int m = 0; m < 4; ++m) o_acc[h][m] *= a;
+        m_run[h] = m_tile[h];
+      }
+      shift[h] = m_run[h];
+      rsum[h] = 0.0f;
+      tmax[h] = -INFINITY;
+    }
+    auto expo = [&](int h, int e) {
+      px[h][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[h][e], c2, -shift[h]));
+      rsum[h] += px[h][e];
+    };
+    bf16x8 kf[8], va[8];
+    for (int k = 0; k < 3; ++k) kf[k] = *reinterpret_cast<const bf16x8*>(kr + k_off[k]);
+    const unsigned src_base = (unsigned)((it * 64 + wave * kDma) % 1920) * 1024;  // < 2 MB - 64 KB
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+#pragma unroll
+      for (int j = 0; j < kDma / 8; ++j) {
+        const int i = k * (kDma / 8) + j;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, LDS_PTR(kw + ((wave * kDma + i) % 32) * 1024), 16,
+                                                 src_base + i * 1024 + lane * 16, 0, 0, 0);
+      }
+      if (k + 3 < 8) kf[k + 3] = *reinterpret_cast<const bf16x8*>(kr + k_off[k + 3]);
+      else va[k - 5] = v_pair(vr, v_off, k - 5);
+#pragma unroll
+      for (int h = 0; h < H2; ++h)
+        s_nxt[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qreg[h][k], k == 0 ? f32x16{} : s_nxt[h], 0, 0, 0);
+#pragma unroll
+      for (int h = 0; h < H2; ++h) {
+        expo(h, k);
+        if ((k & 1) == 0) expo(h, 8 + (k >> 1));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    bf16x8 pb[H2][2];
+    for (int h = 0; h < H2; ++h)
+      for (int e = 0; e < 8; ++e) pb[h][0][e] = (__bf16)px[h][e];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k + 3 < 8) va[k + 3] = v_pair(vr, v_off, k + 3);
+#pragma unroll
+      for (int h = 0; h < H2; ++h) {
+        if (k < 4) {
+          expo(h, 12 + k);
+          if (k == 3)
+            for (int e = 8; e < 16; ++e) pb[h][1][e - 8] = (__bf16)px[h][e];
+        }
+        o_acc[h][k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[k], pb[h][k >> 2], o_acc[h][k & 3], 0, 0, 0);
+        tmax[h] = fmaxf(fmaxf(tmax[h], s_nxt[h][2 * k]), s_nxt[h][2 * k + 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int h = 0; h < H2; ++h) {
+      l_run[h] += rsum[h];
+      const unsigned u = __float_as_uint(tmax[h]);
+      const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      m_tile[h] = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])) * c2;
+    }
+  };
+  for (int it = 0; it < iters; it += 2) {  // iters is even
+    iteration(it, s_a, s_b, k1, v0, k0);
+    iteration(it + 1, s_b, s_a, k0, v1, k1);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  float s = 0.0f;
+  for (int h = 0; h < H2; ++h) {
+    s += l_run[h] + m_run[h];
+    for (int m = 0; m < 4; ++m)
+      for (int e = 0; e < 16; ++e) s += o_acc[h][m][e];
+  }
+  sink[blockIdx.x * 512 + threadIdx.x] = s;
+  const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    clocks[2 * blockIdx.x] = c1 - c0;
+    clocks[2 * blockIdx.x + 1] = r1 - r0;
+  }
+}
+
 struct Timer {
   hipEvent_t start, stop;
   Timer() {
@@ -242,6 +388,43 @@ void probe_mfma_valu(float* sink, int threads) {
               kExp ? "v_exp_f32" : "v_fma_f32", ms * 1e6 / mfma_per_simd);
 }
 
+template <int H2>
+void probe_loop_body(const char* src, float* sink, unsigned long long* clocks, const char* data) {
+  const int iters = 1000;
+  Timer t;
+  float best = 1e30f;
+  for (int r = 0; r < 3; ++r) {
+    best = std::min(best, t.ms([&] { hipLaunchKernelGGL((loop_body<H2>), dim3(kCUs), dim3(512 / H2), 0, 0, src,
+                                                        sink, iters, clocks); }));
+  }
+  unsigned long long h[2 * kCUs];
+  CHECK(hipMemcpy(h, clocks, sizeof(h), hipMemcpyDeviceToHost));
+  double cycles = 0, ticks100 = 0;
+  for (int i = 0; i < kCUs; ++i) {
+    cycles += double(h[2 * i]);
+    ticks100 += double(h[2 * i + 1]);
+  }
+  std::printf("loop_body  %d head(s)/wave, %d waves/CU, K/V %-6s: %.3f us per iteration, shader clock %4.0f MHz, "
+              "%4.0f cycles per iteration (MFMA alone: 1024)\n",
+              H2, 8 / H2, data, best * 1e3 / iters, cycles / ticks100 * 100.0, cycles / kCUs / iters);
+}
+
+// Random bf16 values in [-1, 1) over the source buffer (a fixed LCG, so every run sees the same data).
+void fill_random_bf16(char* src) {
+  const size_t count = (kSourceBytes + 1024) / 2;
+  unsigned short* host = static_cast<unsigned short*>(std::malloc(count * 2));
+  unsigned x = 12345u;
+  for (size_t i = 0; i < count; ++i) {
+    x = x * 1664525u + 1013904223u;
+    const float f = float((x >> 8) & 0xFFFF) / 32768.0f - 1.0f;
+    unsigned u;
+    std::memcpy(&u, &f, 4);
+    host[i] = (unsigned short)(u >> 16);
+  }
+  CHECK(hipMemcpy(src, host, count * 2, hipMemcpyHostToDevice));
+  std::free(host);
+}
+
 }  // namespace
 
 int main() {
@@ -272,6 +455,13 @@ int main() {
     probe_mfma_valu<4, false>(sink, threads);
     probe_mfma_valu<8, false>(sink, threads);
   }
+  unsigned long long* clocks = nullptr;
+  CHECK(hipMalloc(&clocks, 2 * kCUs * sizeof(unsigned long long)));
+  probe_loop_body<1>(src, sink, clocks, "zeros");
+  fill_random_bf16(src);
+  probe_loop_body<1>(src, sink, clocks, "random");
+  probe_loop_body<2>(src, sink, clocks, "random");
+  CHECK(hipFree(clocks));
   CHECK(hipFree(src));
   CHECK(hipFree(sink));
   CHECK(hipFree(ticks));
