@@ -858,9 +858,22 @@ def kv_write_bench(args, chunks, k, v, bt, dev):
         return s.elapsed_time(e) * 1000.0 / reps
 
     c0, s0 = chunks[len(chunks) // 2], slots[len(chunks) // 2]
+    # eager calls: bound by the host's enqueue rate (one torch op per chunk)
     us_chunk = per_call_us(lambda: op(k_tok[c0.query_start:c0.seq_len], v_tok[c0.query_start:c0.seq_len], kc, vc, s0))
     all_slots = chunk_slot_mapping(btd, 0, args.prompt)
     us_prompt = per_call_us(lambda: op(k_tok, v_tok, kc, vc, all_slots))
+
+    # device time: every chunk's write replayed as one HIP graph, as a captured prefill step would run them
+    def all_chunks():
+        for c, sl in zip(chunks, slots):
+            op(k_tok[c.query_start:c.seq_len], v_tok[c.query_start:c.seq_len], kc, vc, sl)
+
+    graph = graph_of(all_chunks)
+    us_chunk_graph = per_call_us(graph.replay, reps=20) / len(chunks)
+    torch.cuda.synchronize()
+    if not (torch.equal(kc.view(-1, 8, 128)[logical.to(dev)], k_tok) and
+            torch.equal(vc.view(-1, 8, 128)[logical.to(dev)], v_tok)):
+        raise RuntimeError("paged KV write replayed from a graph does not reproduce the cache")
     moved = lambda tokens: tokens * 8 * 128 * 2 * 2 * 2  # K and V rows, read and written
     gbs_chunk = moved(c0.query_tokens) / (us_chunk * 1e-6) / 1e9
     gbs_prompt = moved(args.prompt) / (us_prompt * 1e-6) / 1e9
@@ -868,6 +881,8 @@ def kv_write_bench(args, chunks, k, v, bt, dev):
         "chunk_tokens": c0.query_tokens,
         "us_per_chunk": round(us_chunk, 2),
         "gbs_chunk": round(gbs_chunk, 1),
+        "us_per_chunk_graph": round(us_chunk_graph, 2),
+        "gbs_chunk_graph": round(moved(c0.query_tokens) / (us_chunk_graph * 1e-6) / 1e9, 1),
         "prompt_tokens": args.prompt,
         "us_prompt": round(us_prompt, 2),
         "gbs_prompt": round(gbs_prompt, 1),

@@ -161,10 +161,13 @@ def test_config2_full_prefill(gpu):
 
 
 def test_config3_outliers_chunk2048(gpu):
-    """Config 3 (L=8320, chunk 2048, +-8 outliers in 1% of K): two chunks."""
+    """Config 3 (L=8320, chunk 2048, +-8 outliers in 1% of K): all five chunks, in order -- chunk 0 holds
+    the dense prefix and the 521 crossing, the last one the 128 dense tail rows."""
     k, v, bt = make_cache(8320, 11, std=1.0, outlier_frac=0.01)
     qfull = make_query(8320, 12, std=1.0)
-    for c in (prompt_chunks(8320, 2048)[1], prompt_chunks(8320, 2048)[-1]):
+    chunks = prompt_chunks(8320, 2048)
+    assert len(chunks) == 5 and chunks[0].query_start == 0 and chunks[-1].seq_len == 8320
+    for c in chunks:
         q = qfull[c.query_start:c.seq_len].contiguous()
         expected = OA.attention_torch(q, k, v, bt, c.query_start, c.seq_len, c.prompt_len, SCALE)
         actual = _run_sparse(q, k, v, bt, c.query_start, c.seq_len, c.prompt_len, gpu)
