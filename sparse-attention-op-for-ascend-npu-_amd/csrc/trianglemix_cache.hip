@@ -35,10 +35,13 @@ paged_kv_write_kernel(const uint4* __restrict__ key, const uint4* __restrict__ v
   const int64_t token = g / kChunksPerRow;
   const int chunk = (int)(g % kChunksPerRow);
   if (token >= num_tokens) return;
-  const int64_t slot = slot_mapping[token];
-  if (slot < 0 || slot >= num_slots) return;
+  // The K / V loads do not depend on the slot: issued together with the slot
+  // load, the two memory round trips overlap instead of following each other
+  // (the compiler cannot hoist loads above the slot test by itself).
   const uint4 k = key[token * key_stride_chunks + chunk];
   const uint4 v = value[token * value_stride_chunks + chunk];
+  const int64_t slot = slot_mapping[token];
+  if (slot < 0 || slot >= num_slots) return;
   key_cache[slot * kChunksPerRow + chunk] = k;
   value_cache[slot * kChunksPerRow + chunk] = v;
 }
