@@ -78,8 +78,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-legs", action="store_true", help="headline only (skip the config 1/3/4/5 legs)")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--only", choices=("sparse", "dense"), help="run one kernel only (for profiling)")
-    ap.add_argument("--workload", choices=("config1", "config2", "config3", "config4", "config5"),
-                    default="config2")
+    ap.add_argument("--workload", choices=("config1", "config2", "config3", "config4", "config5", "host"),
+                    default="config2", help="host: host time per call of each API level (one middle chunk)")
     ap.add_argument("--outliers", type=float, default=None, help="fraction of K entries set to +-8")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run 5 plain device copies of MIB MiB (scales rocprofv3 FETCH/WRITE_SIZE)")
@@ -101,6 +101,8 @@ def main() -> int:
         return config4_curve(args)
     if args.workload == "config5":
         return config5_stack(args)
+    if args.workload == "host":
+        return host_overhead(args)
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     native.load_hip_library()
     native.load_triangle_mix_adapter()
@@ -760,6 +762,93 @@ def layer_stack_summary(seed: int) -> dict:
     del stack
     torch.cuda.empty_cache()
     return out
+
+
+def host_overhead(args) -> int:
+    """Host time per call of one config-2 middle chunk at each API level, beside the kernel's device time.
+
+    Each level is called 100 times back to back with no synchronisation inside the timed loop, so the time
+    is what the host spends per call; events around the same calls give the rate the GPU sees (the larger
+    of host and device time).  The device time comes from a HIP graph of 16 launches.
+    """
+    import torch
+
+    from trianglemix import cabi, kernel, native
+    from trianglemix.config import resolve_plugin_config
+    from trianglemix.planning import build_batch_plan
+    from trianglemix.router import TriangleMixRouter
+    from trianglemix.stats import TriangleMixRuntimeStats
+    from trianglemix.workload import SCALE, make_cache, make_query
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    native.load_hip_library()
+    native.load_triangle_mix_adapter()
+    dev = torch.device("cuda:0")
+    qs, tq, prompt = 4096, 512, 8192
+    seq = qs + tq
+    k, v, bt = make_cache(seq, args.seed, std=1.0)
+    q = make_query(tq, args.seed + 1, std=1.0)
+    kd, vd, btd, qd = k.to(dev), v.to(dev), bt.to(dev), q.to(dev)
+    out = torch.empty_like(qd)
+
+    def router_for(layers: str):
+        class _Vllm:
+            additional_config = {"trianglemix": {"enabled": True, "layers": layers}}
+
+        cfg = resolve_plugin_config(_Vllm())
+        return cfg, TriangleMixRouter(cfg, stats=TriangleMixRuntimeStats())
+
+    cfg, router = router_for("0-35")
+    _, dense_router = router_for("5")
+    plan = build_batch_plan(state_name="ChunkedPrefill", cumulative_query_ends=[tq], seq_lens=[seq],
+                            prompt_lens=[prompt], num_decodes=0, num_prefills=1, config=cfg.kernel)
+    routed = dict(plan=plan, query=qd, key_cache=kd, value_cache=vd, block_table=btd, output=out, softmax_scale=SCALE)
+    levels = {
+        "torch_op": lambda: torch.ops.trianglemix.triangle_paged_sparse_attention.out(
+            qd, kd, vd, btd, qs, seq, prompt, SCALE, out=out),
+        "c_abi_ctypes": lambda: cabi.triangle_paged_sparse_attention(
+            qd, kd, vd, btd, out, query_start=qs, seq_len=seq, prompt_len=prompt, scale=SCALE),
+        "python_op": lambda: kernel.triangle_direct_paged_attention(
+            query=qd, key_cache=kd, value_cache=vd, block_table=btd, seq_len=seq, prompt_len=prompt, output=out,
+            softmax_scale=SCALE, config=cfg.kernel),
+        "router_direct": lambda: router.prefill_attention(layer_name="model.layers.5.self_attn.attn", **routed),
+        "router_dense_layer": lambda: dense_router.prefill_attention(layer_name="model.layers.6.self_attn.attn",
+                                                                     **routed),
+    }
+    result = {}
+    for name, fn in levels.items():
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        host = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            for _ in range(100):
+                fn()
+            host.append((time.perf_counter() - t0) * 1e4)
+            torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(100):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        result[name] = {"host_us_per_call": round(statistics.median(host), 2),
+                        "stream_us_per_call": round(s.elapsed_time(e) * 10, 2)}
+    graph = graph_of(lambda: [levels["torch_op"]() for _ in range(16)])
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(10):
+        graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    print(json.dumps({
+        "metric": "host time per attention call (one middle chunk, L=8192 chunk 512)", "unit": "us/call",
+        "n_gpus": 1, "higher_is_better": False, "data": "synthetic",
+        "config": {"workload": "host: qs=4096 tq=512 prompt=8192, 100 calls per level, median of 5 windows"},
+        "levels": result, "device_us_per_call": round(s.elapsed_time(e) * 1000 / 160, 2),
+    }), flush=True)
+    return 0
 
 
 def config5_stack(args) -> int:

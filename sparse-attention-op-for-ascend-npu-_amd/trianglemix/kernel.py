@@ -14,7 +14,9 @@ and errors:
 * ``estimate_tile_counts`` (kernel.py:492-522)
 
 plus the dense paged causal companion ``dense_paged_causal_attention`` that
-replaces the reference's official FIA fallback.  There is no CPU path: the
+replaces the reference's official FIA fallback, and
+``triangle_direct_after_gates``, the router's launch of a call that passed its
+gates (the public function without the Python re-checks).  There is no CPU path: the
 ops exist only for ROCm device tensors and the native adapter must be loaded.
 """
 
@@ -254,6 +256,31 @@ def triangle_direct_paged_attention(*, query, key_cache, value_cache, block_tabl
     _run_triangle_single_launch_out(query=query, key_cache=key_cache, value_cache=value_cache,
                                     block_table=block_table, query_start=span.q0, seq_len=span.q1,
                                     prompt_len=prompt_len, softmax_scale=softmax_scale, output=output)
+    return output
+
+
+_SPARSE_OUT = None  # torch.ops.trianglemix.triangle_paged_sparse_attention.out, looked up once
+
+
+def triangle_direct_after_gates(*, query, key_cache, value_cache, block_table, seq_len: int, prompt_len: int,
+                                output, softmax_scale: float, config: TriangleMixConfig):
+    """The router's direct launch: ``triangle_direct_paged_attention`` without its Python pre-checks.
+
+    Only for a call that passed the router's gates (``router.dispatch_reason``):
+    the planner's sparse-middle gate, the geometry gate, the adapter gate and
+    the query / output / KV cache / block table gates cover every check of the
+    public function, so repeating them on each of a step's layer calls is
+    host time the GPU waits for.  The op still validates every tensor in C++
+    before it launches.
+    """
+    global _SPARSE_OUT
+    op = _SPARSE_OUT
+    if op is None:
+        import torch
+
+        op = _SPARSE_OUT = torch.ops.trianglemix.triangle_paged_sparse_attention.out
+    op(query, key_cache, value_cache, block_table, seq_len - query.shape[0], seq_len, prompt_len, softmax_scale,
+       out=output)
     return output
 
 

@@ -34,7 +34,7 @@ from .kernel import (
     SUPPORTED_QUERY_HEADS,
     dense_paged_causal_attention,
     extract_layer_index,
-    triangle_direct_paged_attention,
+    triangle_direct_after_gates,
 )
 from .native import triangle_mix_adapter_loaded
 from .planning import FallbackReason, TriangleBatchPlan
@@ -138,6 +138,51 @@ def _block_table_reason(block_table: object, query: object, seq_len: int) -> Fal
     return FallbackReason.NONE
 
 
+_TORCH_TYPES: tuple | None = None  # (torch.Tensor, torch.bfloat16, torch.int32) once torch is imported
+
+
+def _torch_types() -> tuple:
+    global _TORCH_TYPES
+    if _TORCH_TYPES is None:
+        import torch
+
+        _TORCH_TYPES = (torch.Tensor, torch.bfloat16, torch.int32)
+    return _TORCH_TYPES
+
+
+def _tensor_reason(features: LayerFeatures, query, output, key_cache, value_cache, block_table,
+                   query_len: int, seq_len: int) -> FallbackReason:
+    """The query / output, KV cache and block table gates for torch tensors whose query is on a GPU, with
+    the same predicates and order as ``_query_reason``, ``_kv_reason`` and ``_block_table_reason`` but read
+    straight from the tensors (each routed call pays these checks).  Devices compare by index: with the
+    query on a GPU, a tensor on the same device has the same index and any other tensor another index
+    (-1 off the GPU)."""
+    _, bf16, i32 = _torch_types()
+    qs = query.shape
+    if (len(qs) != 3 or qs[1] != SUPPORTED_QUERY_HEADS or qs[2] != SUPPORTED_HEAD_SIZE or qs[0] != query_len
+            or query.dtype is not bf16 or not query.is_contiguous() or features.num_heads != SUPPORTED_QUERY_HEADS
+            or features.num_kv_heads != SUPPORTED_KV_HEADS or features.head_size != SUPPORTED_HEAD_SIZE):
+        return FallbackReason.QUERY_UNSUPPORTED
+    device = query.get_device()
+    os_ = output.shape
+    if (not os_ or os_[0] < qs[0] or output.dtype is not bf16 or output.get_device() != device
+            or not output.is_contiguous()):
+        return FallbackReason.QUERY_UNSUPPORTED
+    ks = key_cache.shape
+    if (len(ks) != 4 or ks[1] != SUPPORTED_CACHE_BLOCK_SIZE or ks[2] != SUPPORTED_KV_HEADS
+            or ks[3] != SUPPORTED_HEAD_SIZE or value_cache.shape != ks or key_cache.dtype is not bf16
+            or value_cache.dtype is not bf16 or key_cache.get_device() != device
+            or value_cache.get_device() != device or not key_cache.is_contiguous()
+            or not value_cache.is_contiguous()):
+        return FallbackReason.KV_CACHE_UNSUPPORTED
+    bs = block_table.shape
+    if (len(bs) != 2 or bs[0] != 1 or bs[1] < -(-seq_len // SUPPORTED_CACHE_BLOCK_SIZE)
+            or block_table.dtype is not i32 or block_table.get_device() != device
+            or not block_table.is_contiguous()):
+        return FallbackReason.BLOCK_TABLE_UNSUPPORTED
+    return FallbackReason.NONE
+
+
 def dispatch_reason(*, config: PluginConfig, plan: TriangleBatchPlan, features: LayerFeatures, query: object,
                     output: object, key_cache: object, value_cache: object, block_table: object,
                     capturing: bool, native_ready: bool) -> FallbackReason:
@@ -148,8 +193,16 @@ def dispatch_reason(*, config: PluginConfig, plan: TriangleBatchPlan, features: 
         return plan.primary_reason
     if not native_ready:
         return FallbackReason.ADAPTER_UNAVAILABLE
-    for reason in (_model_reason(features, config), _query_reason(features, query, output, plan),
-                   _kv_reason(key_cache, value_cache, query)):
+    reason = _model_reason(features, config)
+    if reason is not FallbackReason.NONE:
+        return reason
+    tensor = _torch_types()[0]
+    if (type(query) is tensor and type(output) is tensor and type(key_cache) is tensor
+            and type(value_cache) is tensor and type(block_table) is tensor and query.is_cuda):
+        request = plan.requests[0]
+        return _tensor_reason(features, query, output, key_cache, value_cache, block_table, request.query_len,
+                              request.seq_len)
+    for reason in (_query_reason(features, query, output, plan), _kv_reason(key_cache, value_cache, query)):
         if reason is not FallbackReason.NONE:
             return reason
     return _block_table_reason(block_table, query, plan.requests[0].seq_len)
@@ -158,12 +211,13 @@ def dispatch_reason(*, config: PluginConfig, plan: TriangleBatchPlan, features: 
 class TriangleMixRouter:
     """Routes one layer's prefill attention for the current scheduler step.
 
-    ``direct_fn`` / ``dense_fn`` default to the gfx950 ops; tests substitute
-    them to force failure paths on the CPU.
+    ``direct_fn`` / ``dense_fn`` default to the gfx950 ops (the direct one
+    without the Python pre-checks the router's gates already made); tests
+    substitute them to force failure paths on the CPU.
     """
 
     def __init__(self, config: PluginConfig, *, stats: TriangleMixRuntimeStats | None = None,
-                 direct_fn: Callable[..., Any] = triangle_direct_paged_attention,
+                 direct_fn: Callable[..., Any] = triangle_direct_after_gates,
                  dense_fn: Callable[..., Any] = dense_paged_causal_attention,
                  native_ready: Callable[[], bool] = triangle_mix_adapter_loaded) -> None:
         self.config = config
@@ -202,16 +256,14 @@ class TriangleMixRouter:
         writes the chunk's K/V into the cache there).  A failure in either
         one, like a failing launch, is counted and falls back.
         """
-        seq_len = plan.requests[0].seq_len if plan is not None else None
-        dense_kwargs = dict(query=query, key_cache=key_cache, value_cache=value_cache, block_table=block_table,
-                            output=output, scale=softmax_scale)
-
         def dense():
             if fallback is not None:
                 return fallback()
-            if seq_len is None:
+            if plan is None:
                 raise ValueError("dense fallback needs the chunk's seq_len from a plan")
-            return self._dense_fallback(seq_len=seq_len, **dense_kwargs)
+            return self._dense_fallback(query=query, key_cache=key_cache, value_cache=value_cache,
+                                        block_table=block_table, output=output, scale=softmax_scale,
+                                        seq_len=plan.requests[0].seq_len)
 
         if not self.config.enabled or plan is None or not self.config.kernel.uses_layer(layer_name):
             return dense()

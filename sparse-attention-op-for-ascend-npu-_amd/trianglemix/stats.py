@@ -358,6 +358,8 @@ class TriangleMixRuntimeStats:
     # ------------------------------------------------------------- reading
     def structured_log_if_due(self) -> dict[str, Any] | None:
         """This worker's counters plus the plan events buffered since the last flush, when a flush applies."""
+        if not self._log.interval:  # logging off (the default): nothing is ever buffered or due
+            return None
         with self._lock:
             taken = self._log.take(self._tallies.counters["request_total"])
             if taken is None:

@@ -291,7 +291,7 @@ def config_of(owner: object) -> PluginConfig:
 class SeamOps:
     """The device calls of the direct path (tests substitute them on the CPU)."""
 
-    direct: Callable[..., Any] | None = None      # default: kernel.triangle_direct_paged_attention
+    direct: Callable[..., Any] | None = None      # default: the router's (kernel.triangle_direct_after_gates)
     kv_write: Callable[..., Any] | None = None    # default: cache.reshape_and_cache
     native_ready: Callable[[], bool] | None = None
 

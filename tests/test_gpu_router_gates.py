@@ -1,0 +1,91 @@
+"""The router's gates on GPU tensors: the fast path equals the generic predicates.
+
+``router.dispatch_reason`` reads torch tensors whose query is on a GPU
+through ``_tensor_reason`` (direct attribute reads, device indices) and
+everything else through ``_query_reason`` / ``_kv_reason`` /
+``_block_table_reason`` (the restatement of the reference's
+``_validate_query`` / ``_validate_static_kv`` / ``_validate_block_table``,
+plugin.py:1106-1192).  For a well-formed call and for one broken property at
+a time -- dtype, shape, row count, contiguity, device, block-table length --
+both must name the same reason.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from trianglemix import router as R
+from trianglemix.config import PluginConfig
+from trianglemix.kernel import TriangleMixConfig
+from trianglemix.planning import FallbackReason, build_batch_plan
+
+pytestmark = pytest.mark.gpu
+
+
+def _generic(features, plan, query, output, key_cache, value_cache, block_table):
+    for reason in (R._query_reason(features, query, output, plan), R._kv_reason(key_cache, value_cache, query)):
+        if reason is not FallbackReason.NONE:
+            return reason
+    return R._block_table_reason(block_table, query, plan.requests[0].seq_len)
+
+
+def _variants(dev):
+    tq, seq, prompt = 512, 4608, 8192
+    pages = 40
+    base = dict(query=torch.zeros(tq, 32, 128, dtype=torch.bfloat16, device=dev),
+                output=torch.zeros(tq + 16, 32, 128, dtype=torch.bfloat16, device=dev),
+                key_cache=torch.zeros(pages, 128, 8, 128, dtype=torch.bfloat16, device=dev),
+                value_cache=torch.zeros(pages, 128, 8, 128, dtype=torch.bfloat16, device=dev),
+                block_table=torch.zeros(1, 36, dtype=torch.int32, device=dev))
+    cases = [("ok", {})]
+    cases += [
+        ("query fp16", {"query": base["query"].half()}),
+        ("query rows", {"query": torch.zeros(tq - 1, 32, 128, dtype=torch.bfloat16, device=dev)}),
+        ("query heads", {"query": torch.zeros(tq, 16, 128, dtype=torch.bfloat16, device=dev)}),
+        ("query 2-d", {"query": torch.zeros(tq, 32 * 128, dtype=torch.bfloat16, device=dev)}),
+        ("query strided", {"query": torch.zeros(tq, 32, 256, dtype=torch.bfloat16, device=dev)[:, :, :128]}),
+        ("output short", {"output": torch.zeros(tq - 1, 32, 128, dtype=torch.bfloat16, device=dev)}),
+        ("output fp32", {"output": torch.zeros(tq, 32, 128, dtype=torch.float32, device=dev)}),
+        ("output cpu", {"output": torch.zeros(tq, 32, 128, dtype=torch.bfloat16)}),
+        ("output strided", {"output": torch.zeros(tq, 64, 128, dtype=torch.bfloat16, device=dev)[:, ::2]}),
+        ("output 0-d", {"output": torch.zeros((), dtype=torch.bfloat16, device=dev)}),
+        ("kv page size", {"key_cache": torch.zeros(pages, 64, 8, 128, dtype=torch.bfloat16, device=dev)}),
+        ("kv mismatch", {"value_cache": torch.zeros(pages + 1, 128, 8, 128, dtype=torch.bfloat16, device=dev)}),
+        ("kv fp16", {"value_cache": base["value_cache"].half()}),
+        ("kv cpu", {"key_cache": base["key_cache"].cpu(), "value_cache": base["value_cache"].cpu()}),
+        ("v cpu", {"value_cache": base["value_cache"].cpu()}),
+        ("kv strided", {"key_cache": torch.zeros(pages, 128, 16, 128, dtype=torch.bfloat16, device=dev)[:, :, ::2]}),
+        ("kv 5-d", {"key_cache": base["key_cache"][None], "value_cache": base["value_cache"][None]}),
+        ("table short", {"block_table": torch.zeros(1, 35, dtype=torch.int32, device=dev)}),
+        ("table int64", {"block_table": torch.zeros(1, 36, dtype=torch.int64, device=dev)}),
+        ("table batch 2", {"block_table": torch.zeros(2, 36, dtype=torch.int32, device=dev)}),
+        ("table cpu", {"block_table": torch.zeros(1, 36, dtype=torch.int32)}),
+        ("table strided", {"block_table": torch.zeros(1, 72, dtype=torch.int32, device=dev)[:, ::2]}),
+    ]
+    return base, cases, (tq, seq, prompt)
+
+
+def test_fast_gates_equal_generic_gates(gpu):
+    base, cases, (tq, seq, prompt) = _variants(gpu)
+    kcfg = TriangleMixConfig(enabled=True, layer_indices=frozenset({5}))
+    config = PluginConfig(kernel=kcfg)
+    plan = build_batch_plan(state_name="ChunkedPrefill", cumulative_query_ends=[tq], seq_lens=[seq],
+                            prompt_lens=[prompt], num_decodes=0, num_prefills=1, config=kcfg)
+    assert plan.direct
+    features = R.LayerFeatures()
+    seen = set()
+    for name, change in cases:
+        t = {**base, **change}
+        want = _generic(features, plan, **t)
+        got = R.dispatch_reason(config=config, plan=plan, features=features, capturing=False, native_ready=True,
+                                **t)
+        assert got is want, (name, got, want)
+        seen.add(want)
+    # the cases reach every tensor reason and the well-formed call passes
+    assert seen == {FallbackReason.NONE, FallbackReason.QUERY_UNSUPPORTED, FallbackReason.KV_CACHE_UNSUPPORTED,
+                    FallbackReason.BLOCK_TABLE_UNSUPPORTED}
+    # the layer's head counts are checked with the query, on both paths
+    bad = R.LayerFeatures(num_heads=16)
+    assert R.dispatch_reason(config=config, plan=plan, features=bad, capturing=False, native_ready=True,
+                             **base) is _generic(bad, plan, **base) is FallbackReason.QUERY_UNSUPPORTED
