@@ -1,6 +1,6 @@
 // Hardware probes behind the attention kernel's design (MI355X / gfx950).
 //
-// Three measurements, each over 256 workgroups (one per CU) and printed as one
+// Five measurements, each over 256 workgroups (one per CU) and printed as one
 // table row per configuration:
 //  1. L2 -> CU bandwidth of LDS DMA (buffer_load ... lds, 1 KB per
 //     instruction) against the number of instructions each wave keeps in
@@ -21,6 +21,13 @@
 //     zeros or of random bf16 values; each row gives the time per iteration,
 //     the shader clock over the launch (s_memtime against the 100 MHz
 //     s_memrealtime) and the cycles per iteration.
+//  5. MFMA alone at full load: back-to-back v_mfma_f32_32x32x16_bf16 into
+//     four independent accumulators, operands read once from the zero or
+//     random buffer, at 1 and 2 waves per SIMD.  Each row gives the MFMA
+//     rate as chip TFLOP/s and as a fraction of the 2.5 PFLOP/s bf16 peak
+//     (32 cycles per MFMA at 2.4 GHz), beside the shader clock: the power
+//     limit sets the clock, so it is the chip's sustainable MFMA rate for
+//     such operands.
 //
 // Build and run: python -m trianglemix.microbench  (or hipcc --offload-arch=gfx950 -O3 this file).
 
@@ -189,6 +196,37 @@ __global__ void __launch_bounds__(512) mfma_valu(float* sink, int rounds) {
   for (int i = 0; i < 16; ++i) s += acc0[i] + acc1[i];
   for (int i = 0; i < 12; ++i) s += x[i];
   sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// ---- 5. MFMA alone: eight operand pairs per lane (distinct per lane and wave) feed four accumulators.
+__global__ void __launch_bounds__(512) mfma_power(const bf16x8* src, float* sink, int rounds,
+                                                  unsigned long long* clocks) {
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  // 16 operands of 16 B per lane from a 4096-lane window of the source: at most 65,536 of its 131,136.
+  const bf16x8* mine = src + ((blockIdx.x * blockDim.x + threadIdx.x) % 4096) * 16;
+  bf16x8 a[8], b[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    a[k] = mine[k];
+    b[k] = mine[8 + k];
+  }
+  f32x16 acc[4] = {};
+  for (int round = 0; round < rounds; ++round) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k], b[k], acc[k & 3], 0, 0, 0);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += acc[m][i];
+  }
+  sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
+  const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    clocks[2 * blockIdx.x] = c1 - c0;
+    clocks[2 * blockIdx.x + 1] = r1 - r0;
+  }
 }
 
 // ---- 4. The attention loop body, in the kernel's shape (H2 = 1) and with two heads per wave (H2 = 2).
@@ -409,6 +447,28 @@ void probe_loop_body(const char* src, float* sink, unsigned long long* clocks, c
               H2, 8 / H2, data, best * 1e3 / iters, cycles / ticks100 * 100.0, cycles / kCUs / iters);
 }
 
+void probe_mfma_power(const char* src, float* sink, unsigned long long* clocks, int threads, const char* data) {
+  const int rounds = 20000;
+  Timer t;
+  float last = 0.0f;
+  for (int r = 0; r < 3; ++r) {  // the clock settles over the first launches: report the third
+    last = t.ms([&] { hipLaunchKernelGGL(mfma_power, dim3(kCUs), dim3(threads), 0, 0,
+                                         reinterpret_cast<const bf16x8*>(src), sink, rounds, clocks); });
+  }
+  unsigned long long h[2 * kCUs];
+  CHECK(hipMemcpy(h, clocks, sizeof(h), hipMemcpyDeviceToHost));
+  double cycles = 0, ticks100 = 0;
+  for (int i = 0; i < kCUs; ++i) {
+    cycles += double(h[2 * i]);
+    ticks100 += double(h[2 * i + 1]);
+  }
+  const double mfma_per_simd = rounds * 8.0 * (threads / 256);
+  const double tflops = mfma_per_simd * 4 * kCUs * 32768.0 / (last * 1e-3) / 1e12;
+  std::printf("mfma_power waves/SIMD %d, operands %-6s: %6.2f ns per MFMA per SIMD, %6.0f TFLOP/s = %.2f of the "
+              "bf16 peak, shader clock %4.0f MHz\n",
+              threads / 256, data, last * 1e6 / mfma_per_simd, tflops, tflops / 2500.0, cycles / ticks100 * 100.0);
+}
+
 // Random bf16 values in [-1, 1) over the source buffer (a fixed LCG, so every run sees the same data).
 void fill_random_bf16(char* src) {
   const size_t count = (kSourceBytes + 1024) / 2;
@@ -458,9 +518,12 @@ int main() {
   unsigned long long* clocks = nullptr;
   CHECK(hipMalloc(&clocks, 2 * kCUs * sizeof(unsigned long long)));
   probe_loop_body<1>(src, sink, clocks, "zeros");
+  probe_mfma_power(src, sink, clocks, 512, "zeros");
   fill_random_bf16(src);
   probe_loop_body<1>(src, sink, clocks, "random");
   probe_loop_body<2>(src, sink, clocks, "random");
+  probe_mfma_power(src, sink, clocks, 512, "random");
+  probe_mfma_power(src, sink, clocks, 256, "random");
   CHECK(hipFree(clocks));
   CHECK(hipFree(src));
   CHECK(hipFree(sink));

@@ -3,8 +3,10 @@
 ``python -m trianglemix.microbench`` compiles the probes for gfx950 (when the
 binary is missing or older than its source) and runs them on the current GPU:
 L2 -> CU bandwidth of LDS DMA and VGPR loads against loads in flight, LDS
-read bandwidth while other waves stream DMA, and MFMA issue rate with
-independent VALU instructions between MFMAs.
+read bandwidth while other waves stream DMA, MFMA issue rate with independent
+VALU instructions between MFMAs, the attention loop body's time and shader
+clock on zero and random K/V, and the chip's MFMA rate and clock at full load
+on zero and random operands.
 """
 
 from __future__ import annotations
