@@ -344,9 +344,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   const int tb = p.query_start + rb * kRowBlock;
   const int te = min(tb + kRowBlock, p.seq_len);
   const int hq = H * hp + hl;  // query head inside the GQA group
-  const int head = kvh * kGroup + hq;
   const int q = tb + n;
-  const bool row_active = q < te;
 
   const TileRuns runs = row_block_tiles(tb, te, sparse_begin, sparse_end);
   const int all_tiles = runs.count();
@@ -829,13 +827,29 @@ triangle_paged_attention_kernel(KernelParams p) {
     m_run = mt;
   }
 
+  // Stores that must reach the level where every L2 of the GPU is coherent
+  // (agent scope): the output rows and the split partials.
+  constexpr int kCpolAgent = 16;  // sc1
   // Normalise the O merged d-blocks (row sum: the two 32-lane halves hold
-  // one row) and store them as bf16, rounded to nearest even.
-  auto store_rows = [&](const f32x16_t* blocks, float l_lane) {
+  // one row), round them to bf16 (nearest even) and store the workgroup's
+  // output as whole rows.  A lane holds 8-byte pieces of one row, so the
+  // pieces are first gathered in LDS: row r of the stage holds the H heads'
+  // 256-byte rows in output order (16-byte chunk c at position c ^ (r % 16),
+  // which spreads the 32 rows' writes over the banks), and then each
+  // instruction stores 64 x 16 B of whole output rows (the H heads of a
+  // token are adjacent in the output), written through L2.  The same number
+  // of bytes as piecewise stores, but in whole cache lines: measured 4-7 %
+  // faster per chunk, most of it from the write-through.  stage is an LDS
+  // region of kRowBlock * H * 256 bytes that no wave still reads.
+  constexpr int kStageRow = H * kRowBytes;
+  constexpr int kChunksPerRow = kStageRow / 16;     // 32 (H = 2) or 64 (H = 4)
+  constexpr int kRowsPerStore = 64 / kChunksPerRow;  // rows per store instruction: 2 or 1
+  constexpr int kStores = kRowBlock / (kRowsPerStore * kWaves);
+  static_assert(kRowsPerStore * kChunksPerRow == 64 && kStores * kRowsPerStore * kWaves == kRowBlock,
+                "the stores cover the row block");
+  auto store_rows = [&](const f32x16_t* blocks, float l_lane, char* stage) {
     const float l_tot = half_sum(l_lane);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (!row_active) return;
-    __bf16* orow = p.out + ((size_t)(q - p.query_start) * kQueryHeads + head) * kHeadDim;
 #pragma unroll
     for (int o = 0; o < O; ++o) {
 #pragma unroll
@@ -843,13 +857,33 @@ triangle_paged_attention_kernel(KernelParams p) {
         bf16x4_t o4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(blocks[o][4 * g + e] * inv);
-        *reinterpret_cast<bf16x4_t*>(orow + 32 * (kq * O + o) + 8 * g + 4 * half) = o4;
+        const int chunk = (hl * (kRowBytes / 16) + 4 * (kq * O + o) + g) ^ (n & 15);
+        *reinterpret_cast<bf16x4_t*>(stage + n * kStageRow + 16 * chunk + 8 * half) = o4;
       }
     }
+    __syncthreads();
+    // Rows past seq_len fall outside the buffer's range: their stores are dropped.
+    const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.out + ((size_t)(tb - p.query_start) * kQueryHeads + kvh * kGroup + H * hp) * kHeadDim), (short)0,
+        (te - tb - 1) * kQueryHeads * kRowBytes + kStageRow, kBufferFlags);
+    const int c = lane % kChunksPerRow;
+#pragma unroll
+    for (int j = 0; j < kStores; ++j) {
+      const int r = (wave * kStores + j) * kRowsPerStore + lane / kChunksPerRow;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + r * kStageRow + 16 * (c ^ (r & 15)));
+      __builtin_amdgcn_raw_buffer_store_b128(v, out_rsrc, (unsigned)(r * kQueryHeads * kRowBytes + 16 * c), 0,
+                                             kCpolAgent);
+    }
   };
+  // Stage: KV quarters use the last iteration's V slot (its reads ended
+  // before the merge barrier; 16 KB of its 32 KB); KV halves need 32 KB and
+  // use q_lds, whose merge reads must end first.
+  static_assert(kRowBlock * kStageRow <= (P == 4 ? S::kSlotBytes : H * kRowBlock * kRowBytes), "stage fits");
+  char* const stage = P == 4 ? ((num_iters & 1) ? v_lds0 : v_lds1) : q_lds;
   TM_PHASE(13);
   if (nsplit == 1) {
-    store_rows(kept, l_run);
+    if constexpr (P == 2) __syncthreads();  // every wave has read its merge blocks from q_lds
+    store_rows(kept, l_run, stage);
     TM_PHASE(14);
     return;
   }
@@ -868,7 +902,6 @@ triangle_paged_attention_kernel(KernelParams p) {
   // writeback and invalidate) is needed.  Each wave waits for its own stores
   // before the workgroup's arrival is counted; the workgroup that counts last
   // has seen every other split arrive after their stores completed.
-  constexpr int kCpolAgent = 16;               // sc1
   constexpr int kStatM = kGroup * 64 * 64;     // row maxima [hq][lane]
   constexpr int kStatL = kGroup * 64 * 65;     // partial row sums [hq][lane]
   const int first = item - split;
@@ -962,7 +995,9 @@ triangle_paged_attention_kernel(KernelParams p) {
     if (s0 == 0) TM_PHASE(18);
   }
   TM_PHASE(19);
-  store_rows(acc, lt);
+  // The stage is free: for KV halves, q_lds was last read before the barrier
+  // ahead of the arrival count.
+  store_rows(acc, lt, stage);
   TM_PHASE(15);
 }
 
