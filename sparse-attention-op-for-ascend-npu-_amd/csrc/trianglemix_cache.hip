@@ -13,7 +13,10 @@
 // HBM-bound scatter: each token moves 2 KB of K and 2 KB of V in and out.
 // One thread per 16-byte chunk of a token's row (128 chunks per token), a
 // wave covering half a token: every load and store is a coalesced 1 KB
-// stretch.
+// stretch.  The stores are written through L2 (sc1): nothing the attention
+// launches after it will read stays dirty in an L2, and the writes stream out
+// during the kernel instead of at its end (measured: 8192 tokens in 8.5 us
+// instead of 11.4, one 512-token chunk 2.66 us instead of 2.85).
 
 #include <hip/hip_runtime.h>
 
@@ -26,6 +29,11 @@ namespace {
 
 constexpr int kCacheThreads = 256;
 constexpr int kChunksPerRow = kKvHeads * kHeadDim * 2 / 16;  // 16-byte chunks per token row (128)
+static_assert(kCacheThreads % kChunksPerRow == 0 && kChunksPerRow % 64 == 0, "a wave stays inside one token");
+constexpr int kRawBufferFlags = 0x00020000;  // buffer resource word 3 for raw byte-addressed access
+constexpr int kCpolWriteThrough = 16;        // sc1
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(kCacheThreads)
 paged_kv_write_kernel(const uint4* __restrict__ key, const uint4* __restrict__ value, uint4* __restrict__ key_cache,
@@ -40,10 +48,20 @@ paged_kv_write_kernel(const uint4* __restrict__ key, const uint4* __restrict__ v
   // (the compiler cannot hoist loads above the slot test by itself).
   const uint4 k = key[token * key_stride_chunks + chunk];
   const uint4 v = value[token * value_stride_chunks + chunk];
-  const int64_t slot = slot_mapping[token];
+  // A wave covers one token, so its slot is wave-uniform: say so, and the
+  // buffer resources below stay scalar.
+  const int64_t lane_slot = slot_mapping[token];
+  const int64_t slot = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(lane_slot >> 32)) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readfirstlane((int)lane_slot));
   if (slot < 0 || slot >= num_slots) return;
-  key_cache[slot * kChunksPerRow + chunk] = k;
-  value_cache[slot * kChunksPerRow + chunk] = v;
+  const __amdgpu_buffer_rsrc_t k_row = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(key_cache + slot * kChunksPerRow), (short)0, kChunksPerRow * 16, kRawBufferFlags);
+  const __amdgpu_buffer_rsrc_t v_row = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(value_cache + slot * kChunksPerRow), (short)0, kChunksPerRow * 16, kRawBufferFlags);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, k), k_row, (unsigned)(chunk * 16), 0,
+                                         kCpolWriteThrough);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), v_row, (unsigned)(chunk * 16), 0,
+                                         kCpolWriteThrough);
 }
 
 }  // namespace
