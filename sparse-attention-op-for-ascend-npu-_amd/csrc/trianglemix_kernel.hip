@@ -23,6 +23,9 @@
 // partial (O, row max, row sum) to the workspace and counts its arrival, and
 // the workgroup that arrives last merges all partials in split order
 // (deterministic) and writes the output -- every chunk is one launch.
+// The output leaves through an LDS stage as whole rows of the workgroup's
+// heads, written through L2 (sc1), so the kernel's end has no dirty output
+// lines to write back.
 // Items are numbered per KV head, heaviest row blocks first; KV head =
 // blockIdx % 8 keeps every workgroup of one KV head on one XCD (workgroups
 // are dispatched round-robin over the 8 XCDs), so both head pairs of a row
