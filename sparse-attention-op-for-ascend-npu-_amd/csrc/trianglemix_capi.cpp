@@ -96,12 +96,16 @@ constexpr int64_t kHalvesDenseMinTiles = 2048;
 // The costs are fitted to a forced-(shape, T) sweep on MI355X (every plan
 // timed after a clock warm-up, in forward, reverse and forward order) of 30
 // chunks: 21 TriangleMix ones (96-2048 rows at the end of 2560-32768-token
-// prompts) and 9 dense-companion ones.  The planned plan is the fastest
-// measured on 26 of them and at most 2.3 us slower on the rest, 4.4 us
-// summed against 18.3 for the previous costs (which kept quarters to one
+// prompts) and 9 dense-companion ones.  At the fit the planned plan was the
+// fastest measured on 26 of them and at most 2.3 us slower on the rest, 4.4
+// us summed against 18.3 for the previous costs (which kept quarters to one
 // round of workgroups and charged every split item for the merge).  Quarters
-// now take the last 512-row chunk of 3584- to 12288-token prompts in up to 1.5
-// rounds: 34.5 us against 37.6 at L = 8192.
+// take the last 512-row chunk of 3584- to 12288-token prompts in up to 1.5
+// rounds: 31.3 us against 32.0 as halves at L = 8192.  Re-swept after the
+// kernel's output store changed: within 0.3 us of the fastest on 24 chunks,
+// 3.3 us behind at worst and 9.3 us in sum (0.8 % of the chunks' time); an
+// integer refit would save 1.7 us of that but move config 1's chunk to a plan
+// measured 0.17 us slower, so the costs stay.
 // T is at least kMinSplitTiles (1024 keys: a split's fp32 partial of 66 KB
 // stays small next to the K/V it reads, 16 KB per 32-key tile) and at most
 // kMaxItemTiles; KV-halves plans of TriangleMix chunks of at most 16 row

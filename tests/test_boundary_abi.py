@@ -311,23 +311,25 @@ def _regret(lib, g):
                          ids=[f"{g['query_start']}+{g['query_tokens']}/{g['seq_len']}/{g['prompt_len']}"
                               for g in SWEEP["geometries"]])
 def test_planned_split_is_near_the_fastest_measured(lib, g):
-    """The planner's choice is the fastest measured plan or close to it (worst measured gap 2.3 us, on the
-    last 512 rows of a 6144-token prompt, where halves over 32 items beat quarters over 20)."""
-    assert _regret(lib, g) <= 2.5
+    """The planner's choice is the fastest measured plan or close to it.  The worst measured gap is 3.3 us,
+    on the last 512 rows of a 6144-token prompt, where halves over 36 items beat quarters over 20; 24 of
+    the 30 chunks are within 0.3 us."""
+    assert _regret(lib, g) <= 3.5
 
 
 def test_planner_regret_over_the_sweep(lib):
-    """Summed over the 30 geometries the planned plans lose 4.4 us to the fastest measured ones (the costs of
-    the previous planner lost 18.3)."""
+    """Summed over the 30 geometries the planned plans lose 9.3 us to the fastest measured ones, 0.8 % of
+    the 1,231 us the 30 chunks take at their fastest (an integer refit of the costs would save 1.7 us of it
+    and move config 1's chunk to a plan measured 0.17 us slower)."""
     total = sum(_regret(lib, g) for g in SWEEP["geometries"])
-    assert total <= 5.0, total
+    assert total <= 10.0, total
 
 
 # (query_start, query_tokens, seq_len, prompt_len) -> (KV parts, tiles per item, items per KV head)
 # for the BASELINE configurations' split chunks.
 BASELINE_PLANS = [
     ((2357, 512, 2869, 2869), (2, 28, 28)),        # config 1
-    ((7680, 512, 8192, 8192), (4, 124, 24)),       # config 2, last chunk: quarters in 1.5 rounds (34.5 us)
+    ((7680, 512, 8192, 8192), (4, 124, 24)),       # config 2, last chunk: quarters in 1.5 rounds (31.3 us)
     ((4096, 512, 4608, 8192), (4, 32, 16)),        # config 2, a middle chunk: one item per row block, no split
     ((6272, 2048, 8320, 8320), (2, 128, 72)),      # config 3
     ((8192, 128, 8320, 8320), (4, 84, 16)),        # config 3, last chunk
