@@ -830,8 +830,11 @@ triangle_paged_attention_kernel(KernelParams p) {
     m_run = mt;
   }
 
-  // Stores that must reach the level where every L2 of the GPU is coherent
-  // (agent scope): the output rows and the split partials.
+  // The sc1 cache policy (agent scope): stores are written through to, and
+  // loads served from, the level where every L2 of the GPU is coherent.  The
+  // split partials need it to be seen across XCDs inside the launch; the
+  // output rows use it so that no dirty output line is left in an L2 for the
+  // end of the kernel to write back.
   constexpr int kCpolAgent = 16;  // sc1
   // Normalise the O merged d-blocks (row sum: the two 32-lane halves hold
   // one row), round them to bf16 (nearest even) and store the workgroup's
