@@ -438,9 +438,12 @@ triangle_paged_attention_kernel(KernelParams p) {
   const unsigned row_hi = lane_row(64 + lane, phys_hi);
   const int bytes_lo = lane_bytes(lane);
   const int bytes_hi = lane_bytes(64 + lane);
-#ifdef TRIANGLEMIX_PHASE_CLOCKS
-  asm volatile("" ::"v"(row_lo), "v"(row_hi));  // the block-table loads have landed
-#endif
+  // The tile tables are complete here, before any tile DMA: left to itself the
+  // compiler sinks the part it needs only for tiles 64-127 into the loop's
+  // preheader, and the wait for its block-table load there would also wait
+  // for the V DMA of iteration 0, which must stay in flight until block 1 of
+  // iteration 0 (below).
+  asm volatile("" ::"v"(row_lo), "v"(row_hi), "v"(bytes_lo), "v"(bytes_hi));
   TM_PHASE(1);
   // Buffer resource of tensor t (0 = K, 1 = V) of tile ti: the tile's key rows
   // of this KV head, range cut at seq_len; a tile past the item's end gets an
@@ -462,13 +465,17 @@ triangle_paged_attention_kernel(KernelParams p) {
     for (int j = 0; j < S::kDmaPerWave; ++j) dma(rsrc, lds_tile, j);
   };
 
-  // Prologue DMA: K and V of iteration 0, K of iteration 1.
+  // Prologue DMA: K of iterations 0 and 1.  V of iteration 0 follows the
+  // first barrier: before iteration 0 a CU streams Q, two K rounds and a V
+  // round at the CU's DMA rate, and V is needed last (block 1 of iteration 0
+  // reads it from step 8 - kReadAhead on), so Q and K take the bandwidth
+  // first.  Iteration 0 then starts once K of iteration 1 has landed
+  // (measured 3 % faster per config-2 chunk than loading V with the K of
+  // iteration 0).
   if (dma_t == 0) {
     issue_tile(dma_u, 0, k_lds0 + dma_u * kTileBytes);
     __builtin_amdgcn_sched_barrier(0);  // K of iteration 1 goes last: the prologue wait leaves it in flight
     issue_tile(P + dma_u, 0, k_lds1 + dma_u * kTileBytes);
-  } else {
-    issue_tile(dma_u, 1, v_lds0 + dma_u * kTileBytes);
   }
 
   // ---- mask geometry ----
@@ -523,18 +530,23 @@ triangle_paged_attention_kernel(KernelParams p) {
     }
   };
 
-  // Q and K of iteration 0 landed; every wave's last tile share (K of
-  // iteration 1, V of iteration 0: neither is read before the barrier that
-  // opens iteration 0, where each wave waits for all of its loads) may still
-  // be in flight.  Only DMA data is published here, so a bare barrier (no
+  // Q and K of iteration 0 landed; the K waves' share of K of iteration 1 may
+  // still be in flight (it is not read before the barrier that opens
+  // iteration 0).  Only DMA data is published here, so a bare barrier (no
   // fence: the fence of __syncthreads would wait for every outstanding load)
-  // suffices.
-  wait_dma_but<S::kDmaPerWave>();
+  // suffices.  Then the V waves issue V of iteration 0 into its slot, which
+  // nothing has touched yet.
+  if (dma_t == 0) {
+    wait_dma_but<S::kDmaPerWave>();
+  } else {
+    wait_dma();
+  }
   __builtin_amdgcn_s_barrier();
+  if (dma_t == 1) issue_tile(dma_u, 1, v_lds0 + dma_u * kTileBytes);
   TM_PHASE(2);
   // Q^T operand: lane (token n, half) holds Q[q][head][16c + 8*half .. +8].
   // Read in one asm block that waits for its own reads: the compiler cannot
-  // tell q_lds from the K slot the K waves' last DMA still writes, and would
+  // tell q_lds from the slots the K and V DMA still write, and would
   // otherwise wait for that DMA here.  The waits above cover the Q DMA (issued
   // before all K/V DMA).
   bf16x8_t qreg[kHeadDim / 16];
@@ -583,11 +595,21 @@ triangle_paged_attention_kernel(KernelParams p) {
   // ti's row max, then [QK^T of tile ti+4 (K slot kr) || exponentials of tile
   // ti], then [PV of tile ti (V slot vr) || mask and row max of tile ti+4];
   // the prefetch of K for iteration it+2 into kw and V for it+1 into vw (one
-  // tile per wave) is spread over the first block.
+  // tile per wave) is spread over the first block.  Iteration 0 runs only when
+  // the item has more than P tiles, so every part has a tile in it and all
+  // waves take its two extra barriers.
   auto iteration = [&](int it, f32x16_t& s_cur, f32x16_t& s_nxt, const char* kr, const char* vr, char* kw,
                        char* vw) {
-    wait_dma();
-    __syncthreads();  // DMA issued one iteration ago landed; slots kw / vw are no longer read
+    if (it == 0) {
+      // K of iteration 1 landed (the K waves' only load in flight); V of
+      // iteration 0 may still be landing: it is published before its first
+      // read in block 1.  The bare barrier does not wait for it.
+      if (dma_t == 0) wait_dma();
+      __builtin_amdgcn_s_barrier();
+    } else {
+      wait_dma();
+      __syncthreads();  // DMA issued one iteration ago landed; slots kw / vw are no longer read
+    }
     if (it < 8) TM_PHASE(4 + it);
     // The two waves of a SIMD (waves w and w + 4) leave the barrier
     // together and the older one issues first, so the younger one ends every
@@ -629,6 +651,14 @@ triangle_paged_attention_kernel(KernelParams p) {
     };
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
+      if (k == 8 - kReadAhead && it == 0) {
+        // The first V read of iteration 0 follows: each V wave waits for its
+        // V of iteration 0 (older than this iteration's prefetch, of which
+        // ceil(k / step) instructions are issued), then the barrier publishes it.
+        constexpr int kStep = 8 / S::kDmaPerWave;
+        if (dma_t == 1) wait_dma_but<(8 - kReadAhead + kStep - 1) / kStep>();
+        __builtin_amdgcn_s_barrier();
+      }
       // one DMA instruction every 8 / kDmaPerWave steps
       if (k % (8 / S::kDmaPerWave) == 0) dma(pf_rsrc, pf_lds, k / (8 / S::kDmaPerWave));
       if (k + kReadAhead < 8) {
