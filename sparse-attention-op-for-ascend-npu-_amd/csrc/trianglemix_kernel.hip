@@ -52,7 +52,9 @@
 // distinct LDS objects and the loop is unrolled by two so every access names
 // its slot statically: the compiler then sees that the prefetch never aliases
 // the tiles being read and does not wait for it.  Each wave waits for its own
-// DMA (vmcnt 0) before the barrier that opens the next iteration.  Each tile
+// DMA (vmcnt 0) before the barrier that opens the next iteration; iteration 0
+// alone publishes its V tiles later, at a barrier before their first read, so
+// that the prologue's DMA serves Q and K first.  Each tile
 // is addressed through a buffer resource whose range stops at seq_len, so key
 // rows past seq_len read as zeros.  LDS rows are 256 B (one key x 128 dims)
 // with the 16-byte chunks XOR-swizzled so both read patterns are bank-conflict
