@@ -977,6 +977,9 @@ def kv_write_bench(args, chunks, k, v, bt, dev):
         "gbs_prompt": round(gbs_prompt, 1),
         "peak_gbs": PEAK_HBM_GBS,
         "frac_hbm_prompt": round(gbs_prompt / PEAK_HBM_GBS, 4),
+        # the repeated whole-prompt calls move the same 67 MB, which stays in the 256 MB Infinity Cache:
+        # the rate is algorithmic bytes over time and can exceed the HBM figure
+        "note": "algorithmic bytes / time; repeated calls keep the working set in the Infinity Cache",
     }
 
 
