@@ -984,7 +984,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   // One pass over the splits, kMergeBatch at a time with all of a batch's
   // loads in flight: a batch that raises the running max rescales what is
   // already summed (the online-softmax rule).  Slots past the last split
-  // take the last split's values again, weighted 0.
+  // take this workgroup's own values again (registers, no load), weighted 0.
   constexpr int kMergeBatch = 4;
   f32x16_t acc[kHeadDim / 32 / 2];
 #pragma unroll
@@ -995,8 +995,8 @@ triangle_paged_attention_kernel(KernelParams p) {
     f32x4_t xs[kMergeBatch][kHeadDim / 32 / 2][4];
 #pragma unroll
     for (int b = 0; b < kMergeBatch; ++b) {
-      const int sb = min(s0 + b, nsplit - 1);
-      if (sb == split) {
+      const int sb = s0 + b;
+      if (sb == split || sb >= nsplit) {
         // This workgroup's own partial: the values it stored are still in
         // registers, so it is not loaded back (the same sums in the same
         // order; measured 0.45 us less on the config-2 last chunk).
