@@ -1,6 +1,6 @@
 // Hardware probes behind the attention kernel's design (MI355X / gfx950).
 //
-// Five measurements, each over 256 workgroups (one per CU) and printed as one
+// Six measurements, each over 256 workgroups (one per CU) and printed as one
 // table row per configuration:
 //  1. L2 -> CU bandwidth of LDS DMA (buffer_load ... lds, 1 KB per
 //     instruction) against the number of instructions each wave keeps in
@@ -28,6 +28,12 @@
 //     (32 cycles per MFMA at 2.4 GHz), beside the shader clock: the power
 //     limit sets the clock, so it is the chip's sustainable MFMA rate for
 //     such operands.
+//  6. The launch floor: 16 launches of a kernel that does next to nothing
+//     (one LDS round trip and one 4-byte store per thread), back to back on
+//     one stream and as one HIP graph, in the attention kernel's workgroup
+//     shape (512 threads, 144 KB of LDS) and in a light one (64 threads,
+//     4 KB).  Each row gives the time per launch: the dispatch ramp, the
+//     drain and the gap between launches that any kernel of that shape pays.
 //
 // Build and run: python -m trianglemix.microbench  (or hipcc --offload-arch=gfx950 -O3 this file).
 
@@ -196,6 +202,15 @@ __global__ void __launch_bounds__(512) mfma_valu(float* sink, int rounds) {
   for (int i = 0; i < 16; ++i) s += acc0[i] + acc1[i];
   for (int i = 0; i < 12; ++i) s += x[i];
   sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// ---- 6. Launch floor: one LDS round trip and one store per thread.
+template <int kLdsBytes, int kThreads>
+__global__ void __launch_bounds__(kThreads) launch_floor(float* sink) {
+  __shared__ float buf[kLdsBytes / 4];
+  buf[threadIdx.x] = float(threadIdx.x);
+  __syncthreads();
+  sink[blockIdx.x * 512 + threadIdx.x] = buf[(threadIdx.x + 1) % kThreads];
 }
 
 // ---- 5. MFMA alone: eight operand pairs per lane (distinct per lane and wave) feed four accumulators.
@@ -469,6 +484,50 @@ void probe_mfma_power(const char* src, float* sink, unsigned long long* clocks, 
               threads / 256, data, last * 1e6 / mfma_per_simd, tflops, tflops / 2500.0, cycles / ticks100 * 100.0);
 }
 
+template <int kLdsBytes, int kThreads>
+void probe_launch_floor(float* sink) {
+  constexpr int kLaunches = 16, kReps = 50;
+  hipStream_t s;
+  CHECK(hipStreamCreate(&s));
+  hipEvent_t a, b;
+  CHECK(hipEventCreate(&a));
+  CHECK(hipEventCreate(&b));
+  auto step = [&] {
+    for (int i = 0; i < kLaunches; ++i)
+      hipLaunchKernelGGL((launch_floor<kLdsBytes, kThreads>), dim3(kCUs), dim3(kThreads), 0, s, sink);
+  };
+  auto per_launch_us = [&](auto run) {
+    run();
+    CHECK(hipStreamSynchronize(s));
+    CHECK(hipEventRecord(a, s));
+    for (int r = 0; r < kReps; ++r) run();
+    CHECK(hipEventRecord(b, s));
+    CHECK(hipEventSynchronize(b));
+    float t = 0.0f;
+    CHECK(hipEventElapsedTime(&t, a, b));
+    return t * 1e3 / (kReps * kLaunches);
+  };
+  const float eager = per_launch_us([&] {
+    step();
+    CHECK(hipGetLastError());
+  });
+  hipGraph_t g;
+  hipGraphExec_t ge;
+  CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeGlobal));
+  step();
+  CHECK(hipStreamEndCapture(s, &g));
+  CHECK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+  const float graph = per_launch_us([&] { CHECK(hipGraphLaunch(ge, s)); });
+  std::printf("launch_floor %3d threads/WG, %3d KB LDS, %d WGs: %5.2f us per launch back to back, %5.2f us per launch "
+              "in a %d-launch HIP graph\n",
+              kThreads, kLdsBytes / 1024, kCUs, eager, graph, kLaunches);
+  CHECK(hipGraphExecDestroy(ge));
+  CHECK(hipGraphDestroy(g));
+  CHECK(hipEventDestroy(a));
+  CHECK(hipEventDestroy(b));
+  CHECK(hipStreamDestroy(s));
+}
+
 // Random bf16 values in [-1, 1) over the source buffer (a fixed LCG, so every run sees the same data).
 void fill_random_bf16(char* src) {
   const size_t count = (kSourceBytes + 1024) / 2;
@@ -525,6 +584,8 @@ int main() {
   probe_mfma_power(src, sink, clocks, 512, "random");
   probe_mfma_power(src, sink, clocks, 256, "random");
   CHECK(hipFree(clocks));
+  probe_launch_floor<147456, 512>(sink);
+  probe_launch_floor<4096, 64>(sink);
   CHECK(hipFree(src));
   CHECK(hipFree(sink));
   CHECK(hipFree(ticks));

@@ -5,8 +5,9 @@ binary is missing or older than its source) and runs them on the current GPU:
 L2 -> CU bandwidth of LDS DMA and VGPR loads against loads in flight, LDS
 read bandwidth while other waves stream DMA, MFMA issue rate with independent
 VALU instructions between MFMAs, the attention loop body's time and shader
-clock on zero and random K/V, and the chip's MFMA rate and clock at full load
-on zero and random operands.
+clock on zero and random K/V, the chip's MFMA rate and clock at full load
+on zero and random operands, and the per-launch floor of a near-empty kernel
+in the attention kernel's workgroup shape, eager and as a HIP graph.
 """
 
 from __future__ import annotations
