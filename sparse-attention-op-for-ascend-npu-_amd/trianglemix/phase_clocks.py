@@ -10,6 +10,7 @@ distribution over waves of the time since the earliest wave started, plus
 the median length of each loop iteration::
 
     python -m trianglemix.phase_clocks --qs 4096 --tq 512 --prompt 8192
+    python -m trianglemix.phase_clocks --qs 7680 --tq 512 --dense   # the dense companion
 
 The stamps sit between phases, and each stamp waits for the scalar clock
 read, so the instrumented kernel runs a few percent slower than the product.
@@ -44,7 +45,7 @@ def library_path() -> Path:
     return Path(__file__).resolve().parent / "libtrianglemix_phase_clocks.so"
 
 
-def run(qs: int, tq: int, prompt: int, seed: int = 7):
+def run(qs: int, tq: int, prompt: int, seed: int = 7, dense: bool = False):
     """Per-wave clocks (µs since the earliest wave's entry, NaN where a wave did not pass a phase)."""
     import numpy as np
     import torch
@@ -59,7 +60,7 @@ def run(qs: int, tq: int, prompt: int, seed: int = 7):
     lib = ctypes.CDLL(str(path))
     lib.tm_phase_clocks_read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
     seq = qs + tq
-    parts, _, items = cabi.chunk_plan(tq, qs, seq, prompt)
+    parts, _, items = cabi.chunk_plan(tq, qs, seq, None if dense else prompt)
     workgroups = items * (16 if parts == 4 else 8)
     if workgroups > WORKGROUPS:
         raise ValueError(f"{workgroups} workgroups: the phase clocks cover {WORKGROUPS}")
@@ -70,8 +71,11 @@ def run(qs: int, tq: int, prompt: int, seed: int = 7):
     out = torch.empty_like(qd)
 
     def launch():
-        cabi.triangle_paged_sparse_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, prompt_len=prompt,
-                                             scale=SCALE)
+        if dense:
+            cabi.dense_paged_causal_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, scale=SCALE)
+        else:
+            cabi.triangle_paged_sparse_attention(qd, kd, vd, btd, out, query_start=qs, seq_len=seq, prompt_len=prompt,
+                                                 scale=SCALE)
 
     for _ in range(20):
         launch()
@@ -99,9 +103,11 @@ def main(argv=None) -> int:
     ap.add_argument("--qs", type=int, default=4096, help="query_start")
     ap.add_argument("--tq", type=int, default=512, help="query tokens")
     ap.add_argument("--prompt", type=int, default=8192, help="prompt_len")
+    ap.add_argument("--dense", action="store_true", help="the dense paged causal companion (prompt_len unused)")
     a = ap.parse_args(argv)
-    rel, (parts, items, workgroups) = run(a.qs, a.tq, a.prompt)
-    print(f"chunk qs={a.qs} tq={a.tq} prompt={a.prompt}: KV parts {parts}, {items} items per KV head, "
+    rel, (parts, items, workgroups) = run(a.qs, a.tq, a.prompt, dense=a.dense)
+    what = "dense companion" if a.dense else f"prompt={a.prompt}"
+    print(f"chunk qs={a.qs} tq={a.tq} {what}: KV parts {parts}, {items} items per KV head, "
           f"{workgroups} workgroups; µs since the earliest wave's entry")
     print(f"{'phase':>16} {'waves':>6} {'min':>7} {'p50':>7} {'p90':>7} {'max':>7}")
     for slot, name in PHASES.items():
