@@ -182,7 +182,12 @@ __device__ __forceinline__ int k_slot(int row, int chunk) { return chunk ^ (row 
 __device__ __forceinline__ int v_slot(int row, int chunk) { return chunk ^ ((row & 3) << 2); }
 
 // Work item -> (row-block order index, split index, split count), computed
-// by every wave with a wave-wide prefix sum over the row blocks' split counts.
+// by every wave from the row blocks' split counts (lane i: row block base + i).
+// The exclusive prefix sum over the lanes needs no cross-lane data move: bit
+// by bit, it adds 2^b times the number of lower lanes whose count has bit b
+// set (v_mbcnt of a ballot).  That is a few VALU and SALU instructions per
+// bit -- six bits cover 63 splits, and a non-negative int has at most 31 --
+// instead of a chain of dependent ds_bpermute round trips.
 __device__ __forceinline__ void decode_item(const KernelParams& p, int sparse_begin, int sparse_end, int item,
                                             int lane, int& order, int& split, int& nsplit) {
   int acc = 0;
@@ -194,20 +199,19 @@ __device__ __forceinline__ void decode_item(const KernelParams& p, int sparse_be
     const int cnt = o < p.num_row_blocks ? row_block_splits(o, p.num_row_blocks, p.query_start, p.seq_len,
                                                             sparse_begin, sparse_end, p.tiles_per_split)
                                          : 0;
-    int incl = cnt;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int t = __shfl_up(incl, d);
-      if (lane >= d) incl += t;
+    int excl = 0;   // items of the row blocks on lower lanes
+    int total = 0;  // items of the 64 row blocks
+    for (int b = 0; __ballot((cnt >> b) != 0) != 0; ++b) {
+      const unsigned long long bit = __ballot(((cnt >> b) & 1) != 0);
+      excl += (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bit >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bit, 0u)) << b;
+      total += __popcll(bit) << b;
     }
-    const int total = __shfl(incl, 63);
     if (item < acc + total) {
-      const bool mine = cnt > 0 && item >= acc + incl - cnt && item < acc + incl;
-      const unsigned long long m = __ballot(mine);
-      const int src = __ffsll(m) - 1;
-      order = __shfl(o, src);
-      split = item - (acc + __shfl(incl - cnt, src));
-      nsplit = __shfl(cnt, src);
+      const bool mine = cnt > 0 && item >= acc + excl && item < acc + excl + cnt;
+      const int src = __ffsll((unsigned long long)__ballot(mine)) - 1;
+      order = base + src;
+      split = item - acc - __builtin_amdgcn_readlane(excl, src);
+      nsplit = __builtin_amdgcn_readlane(cnt, src);
       return;
     }
     acc += total;
