@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TM_ABI_VERSION 2
+#define TM_ABI_VERSION 3
 
 /* Status codes. */
 #define TM_OK 0
@@ -38,12 +38,19 @@ extern "C" {
 #define TM_ERR_WORKSPACE 3        /* workspace too small for this call */
 #define TM_ERR_LAUNCH 4           /* the HIP launch itself failed */
 
-/* A non-empty workspace starts with this many bytes of arrival counters.
- * They must be zero when a workspace is used for the first time (zero-fill
- * it once after allocating it); every call that completes leaves them zero,
- * so one workspace serves any sequence of calls on one stream.  The rest of
- * the workspace is scratch whose contents do not matter. */
+/* A non-empty workspace starts with this many bytes of arrival words, one
+ * per split row block, KV head and workgroup position; the split-KV partials
+ * follow.  A workspace's contents before a call do not matter (as the
+ * reference's workspace, it is scratch): each word carries a tag unique to
+ * the launch that wrote it, and a word with another launch's tag counts as
+ * zero.  One workspace serves any sequence of calls on one stream. */
 #define TM_WORKSPACE_COUNTER_BYTES 65536
+
+/* No call needs more workspace than this (64 MiB): the planner keeps every
+ * chunk's split-KV partials within it, and a chunk whose rows need no split
+ * needs none.  A caller may allocate this once per stream and pass it to
+ * every call. */
+#define TM_MAX_WORKSPACE_BYTES 67108864
 
 /* ABI version of the loaded library (TM_ABI_VERSION it was built with). */
 int tm_abi_version(void);
@@ -69,14 +76,18 @@ const char* tm_last_error(void);
  * (:161-176); validation follows check_inputs/check_output (:29-97) and
  * TilingFunc (operator/op_host/triangle_paged_sparse_attention.cpp:122-237).
  *
+ * Any chunk the attributes allow is accepted: a row of any length runs in
+ * one workgroup, and rows are split across workgroups only to balance the
+ * GPU, within TM_MAX_WORKSPACE_BYTES of workspace.
+ *
  * workspace / workspace_bytes: device scratch of at least
  * tm_triangle_paged_sparse_attention_workspace_size(...) bytes (may be NULL
- * when that size is 0).  Its first TM_WORKSPACE_COUNTER_BYTES hold the
- * arrival counters of row blocks whose keys are split across workgroups
- * (long dense rows): zero on first use, left zero by every completed call.
- * The rest receives their fp32 partials, which the last workgroup of each
- * such row block merges within the same kernel.  Launches that may overlap
- * in time need distinct workspaces.  It must not overlap any input or out.
+ * when that size is 0; never more than TM_MAX_WORKSPACE_BYTES), with any
+ * contents.  Its first TM_WORKSPACE_COUNTER_BYTES hold the arrival words of
+ * row blocks whose keys are split across workgroups (long dense rows); the
+ * rest receives their fp32 partials, which the last workgroup of each such
+ * row block merges within the same kernel.  Launches that may overlap in
+ * time need distinct workspaces.  It must not overlap any input or out.
  */
 int tm_triangle_paged_sparse_attention(
     const void* query, const void* key_cache, const void* value_cache,
@@ -87,8 +98,9 @@ int tm_triangle_paged_sparse_attention(
 
 /*
  * Device scratch bytes the call above needs for these arguments (0 when the
- * whole chunk runs without split-KV partials), or -1 if the arguments are
- * invalid (see tm_last_error).
+ * whole chunk runs without split-KV partials, at most TM_MAX_WORKSPACE_BYTES),
+ * or -1, with the reason in tm_last_error, for exactly the attributes the
+ * call above refuses.
  * Replaces trianglemix_reference::triangle_paged_sparse_attention_workspace_size
  * (operator/torch_adapter/triangle_paged_attention_torch.cpp:180-261).
  */
@@ -100,17 +112,16 @@ int64_t tm_triangle_paged_sparse_attention_workspace_size(
  * The same TriangleMix call for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
  * has no counterpart in the reference.  No call allocates: the split-KV
- * scratch (arrival counters + partials) is a static array of 64 MiB per GPU
- * (every chunk of up to 2048 rows at L <= 32768, of up to 1024 rows at
- * L <= 65536), held until the process ends; a chunk that needs more is refused with
- * TM_ERR_WORKSPACE before any HIP call.  The device address of the array is
- * looked up once per device, with that device current -- call with the
- * stream's device current, as for any launch.  All calls in one process on
- * one GPU share the array: calls that may overlap in time on that GPU (on
- * different streams, or graphs replayed on different streams) race and must
- * not be made.  The counters start zero and each completed call leaves them
- * zero.  Other arguments, results and errors as
- * tm_triangle_paged_sparse_attention.
+ * scratch (arrival words + partials) is a static array of
+ * TM_MAX_WORKSPACE_BYTES (64 MiB) per GPU where the library's code loads,
+ * held until the process ends -- as large as any chunk's workspace, so every
+ * chunk the workspace entry point accepts is accepted here.  The device
+ * address of the array is looked up once per device, with that device
+ * current -- call with the stream's device current, as for any launch.  All
+ * calls in one process on one GPU share the array: calls that may overlap in
+ * time on that GPU (on different streams, or graphs replayed on different
+ * streams) race and must not be made.  Other arguments, results and errors
+ * as tm_triangle_paged_sparse_attention.
  */
 int tm_triangle_paged_sparse_attention_noalloc(
     const void* query, const void* key_cache, const void* value_cache,

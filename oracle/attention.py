@@ -166,6 +166,85 @@ def attention_torch(query, key_cache, value_cache, block_table, query_start: int
     return out
 
 
+def attended_mask(rows, keys, seq_len: int, prompt_len: int, *, dense: bool = False):
+    """Boolean ``[len(rows), len(keys)]``: key ``k`` attended by row ``q``.
+
+    The rule of ``geometry.selected_intervals`` written as a predicate
+    (triangle_v2_reference.py:193-232): ``k < min(q + 1, seq_len)`` and, for a
+    sparse row (``521 <= q < max(0, prompt_len - 128)``), ``k < 8`` or
+    ``k >= q - 512``.  ``rows`` and ``keys`` are int64 torch tensors.
+    """
+    q = rows.reshape(-1, 1)
+    k = keys.reshape(1, -1)
+    keep = k < (q + 1).clamp(max=seq_len)
+    if dense:
+        return keep
+    sparse_end = max(0, prompt_len - G.DENSE_TAIL)
+    sparse = (q >= G.SPARSE_BEGIN) & (q < sparse_end)
+    return keep & (~sparse | (k < G.SINK) | (k >= q - G.WINDOW))
+
+
+def attention_torch_blocked(query, key_cache, value_cache, block_table, query_start: int, seq_len: int,
+                            prompt_len: int, scale: float, *, dense: bool = False, device=None,
+                            max_scores: int = 1 << 26):
+    """float32 restatement of ``torch_reference_attention`` over blocks of rows, on any torch device.
+
+    The same softmax as ``attention_torch`` (one softmax in fp32 over each
+    row's selected keys, then the weighted sum of V), computed for a block of
+    rows at once: the block gathers the keys any of its rows may attend --
+    ``[0, 8)`` plus ``[first_row - 512, last_row]`` when every row is sparse,
+    ``[0, last_row]`` otherwise -- and masks each row with ``attended_mask``.
+    Blocks hold at most ``max_scores`` scores.  Inputs may live on the CPU;
+    the work runs on ``device`` (default: the query's).  Returns fp32
+    ``[Tq, 32, 128]`` on that device.  Pinned against ``attention_torch`` and
+    ``attention_np`` (tests/test_oracle_attention.py).
+    """
+    import torch
+
+    dev = torch.device(device) if device is not None else query.device
+    tq = query.shape[0]
+    if query_start + tq > seq_len:
+        raise ValueError("query rows extend beyond seq_len")
+    pages = -(-seq_len // G.PAGE_SIZE)
+    table = block_table.reshape(-1).to(device=dev, dtype=torch.int64)
+    if table.numel() < pages:
+        raise ValueError("block_table does not cover seq_len")
+    table = table[:pages]
+    # logical K as [8, 128, seq] and V as [8, seq, 128], fp32: a block's keys are slices of them
+    kt = key_cache.to(dev).index_select(0, table).reshape(-1, G.KV_HEADS, G.HEAD_DIM)[:seq_len]
+    kt = kt.float().permute(1, 2, 0).contiguous()
+    vt = value_cache.to(dev).index_select(0, table).reshape(-1, G.KV_HEADS, G.HEAD_DIM)[:seq_len]
+    vt = vt.float().permute(1, 0, 2).contiguous()
+    qf = query.to(dev).float().reshape(tq, G.KV_HEADS, G.GROUP, G.HEAD_DIM)
+    out = torch.empty(tq, G.QUERY_HEADS, G.HEAD_DIM, dtype=torch.float32, device=dev)
+    sparse_end = max(0, prompt_len - G.DENSE_TAIL)
+    r = 0
+    while r < tq:
+        q0 = query_start + r
+        rows = tq - r
+        while rows > 1 and rows * G.QUERY_HEADS * min(q0 + rows, seq_len) > max_scores:
+            rows = (rows + 1) // 2
+        q1 = query_start + r + rows  # rows [q0, q1)
+        if not dense and q0 >= G.SPARSE_BEGIN and q1 <= sparse_end:  # every row sparse
+            lo = max(G.SINK, q0 - G.WINDOW)
+            keys = torch.cat([torch.arange(0, G.SINK, device=dev), torch.arange(lo, q1, device=dev)])
+            k = torch.cat([kt[:, :, :G.SINK], kt[:, :, lo:q1]], dim=2)
+            v = torch.cat([vt[:, :G.SINK], vt[:, lo:q1]], dim=1)
+        else:
+            hi = min(q1, seq_len)
+            keys = torch.arange(0, hi, device=dev)
+            k, v = kt[:, :, :hi], vt[:, :hi]
+        qb = qf[r:r + rows].permute(1, 0, 2, 3).reshape(G.KV_HEADS, rows * G.GROUP, G.HEAD_DIM)
+        s = torch.bmm(qb, k).reshape(G.KV_HEADS, rows, G.GROUP, -1)  # [8, rows, 4, n]
+        mask = attended_mask(torch.arange(q0, q1, device=dev), keys, seq_len, prompt_len, dense=dense)
+        s = s.masked_fill(~mask.reshape(1, rows, 1, -1), float("-inf"))
+        p = torch.softmax(s * float(scale), dim=-1).reshape(G.KV_HEADS, rows * G.GROUP, -1)
+        o = torch.bmm(p, v).reshape(G.KV_HEADS, rows, G.GROUP, G.HEAD_DIM)
+        out[r:r + rows] = o.permute(1, 0, 2, 3).reshape(rows, G.QUERY_HEADS, G.HEAD_DIM)
+        r += rows
+    return out
+
+
 def error_metrics(actual, expected) -> dict:
     """max/mean abs and relative L2 (npu_v2_correctness.py:298-314)."""
     a = np.asarray(actual, dtype=np.float64)

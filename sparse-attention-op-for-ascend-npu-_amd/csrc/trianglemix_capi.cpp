@@ -7,7 +7,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include <unistd.h>
+
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -16,6 +20,9 @@
 
 #include "../../include/trianglemix.h"
 #include "trianglemix_kernel.h"
+
+static_assert(TM_WORKSPACE_COUNTER_BYTES == tmx::kCounterBytes, "the public counter block size is the kernel's");
+static_assert(TM_MAX_WORKSPACE_BYTES == tmx::kMaxWorkspaceBytes, "the public workspace bound is the planner's");
 
 namespace {
 
@@ -107,11 +114,18 @@ constexpr int64_t kHalvesDenseMinTiles = 2048;
 // integer refit would save 1.7 us of that but move config 1's chunk to a plan
 // measured 0.17 us slower, so the costs stay.
 // T is at least kMinSplitTiles (1024 keys: a split's fp32 partial of 66 KB
-// stays small next to the K/V it reads, 16 KB per 32-key tile) and at most
-// kMaxItemTiles; KV-halves plans of TriangleMix chunks of at most 16 row
-// blocks may go down to kFineSplitTiles (768 keys), one more piece per
-// dense-tail row while the items still fit the slots (2-4 % faster on the
-// last 384-512 rows of 2560-4992-token prompts).
+// stays small next to the K/V it reads, 16 KB per 32-key tile); KV-halves
+// plans of TriangleMix chunks of at most 16 row blocks may go down to
+// kFineSplitTiles (768 keys), one more piece per dense-tail row while the
+// items still fit the slots (2-4 % faster on the last 384-512 rows of
+// 2560-4992-token prompts).  The candidates are the ladder kLadderTop,
+// kLadderTop - 4, ... down to that floor (the costs above were fitted on it)
+// and, for rows longer than kLadderTop tiles, every T that cuts the longest
+// row into whole pieces above the ladder, down to one piece (no split).  An
+// item may hold any number of tiles, so rows split for load balance only.
+// A candidate is taken only if its split row blocks' counters and partials
+// fit the workspace bound (tmx::kMaxSplitRowBlocks, tmx::kMaxSplitItems);
+// the no-split plan always does, so every chunk has a plan.
 struct PlanCosts {
   int slots;
   int parts;            // KV parts: tiles per workgroup and iteration
@@ -122,39 +136,97 @@ struct PlanCosts {
 constexpr PlanCosts kQuarterCosts{16, 4, 6, 1, 1};
 constexpr PlanCosts kHalfCosts{32, 2, 5, 3, 1};
 constexpr int kMaxSlots = 32;
-static_assert(kQuarterCosts.slots <= kMaxSlots && kHalfCosts.slots <= kMaxSlots, "simulated_makespan's slot array");
+static_assert(kQuarterCosts.slots <= kMaxSlots && kHalfCosts.slots <= kMaxSlots, "simulated_makespan's slot heap");
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 constexpr int kFineSplitTiles = 768 / tmx::kKvTile;
 // Beyond this many items per candidate the simulation is skipped (its host
 // cost would show): T then spreads the chunk's tiles over one item per slot.
 constexpr int64_t kMaxSimulatedItems = 4096;
-constexpr int kSplitStep = 4;  // candidate T: kMaxItemTiles, kMaxItemTiles - 4, ..., >= the floor
+constexpr int kLadderTop = 128;  // candidate T: kLadderTop, kLadderTop - 4, ..., >= the floor
+constexpr int kSplitStep = 4;
 
+// The row blocks (in issue order, row_tiles[o] tiles each) up to the last one
+// that T splits, and the items they make: the arrival words and partials a
+// launch with this T needs.
+struct SplitLayout {
+  int split_row_blocks;
+  int64_t split_items;
+  int64_t items;
+};
+
+SplitLayout split_layout(const std::vector<int>& row_tiles, int T) {
+  SplitLayout s{0, 0, 0};
+  int64_t before = 0;  // items of the row blocks before o
+  for (size_t o = 0; o < row_tiles.size(); ++o) {
+    const int pieces = (row_tiles[o] + T - 1) / T;
+    before += pieces;
+    if (pieces > 1) {
+      s.split_row_blocks = (int)o + 1;
+      s.split_items = before;
+    }
+  }
+  s.items = before;
+  return s;
+}
+
+bool layout_fits(const SplitLayout& s) {
+  return s.split_row_blocks <= tmx::kMaxSplitRowBlocks && s.split_items <= tmx::kMaxSplitItems;
+}
+
+// Greedy dispatch of the items (issue order) onto the slots, each to the
+// least loaded one (a min-heap of slot loads), in loop iterations.
 int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanCosts& c) {
-  int64_t slot[kMaxSlots] = {};
+  int64_t heap[kMaxSlots] = {};  // all zero: a valid min-heap
+  auto add_to_least = [&](int64_t cost) {
+    int64_t v = heap[0] + cost;  // replace the root, sift down
+    int i = 0;
+    for (;;) {
+      const int l = 2 * i + 1, r = l + 1;
+      int m = i;
+      int64_t mv = v;
+      if (l < c.slots && heap[l] < mv) m = l, mv = heap[l];
+      if (r < c.slots && heap[r] < mv) m = r, mv = heap[r];
+      if (m == i) break;
+      heap[i] = heap[m];
+      i = m;
+    }
+    heap[i] = v;
+  };
   int most_pieces = 1;
   for (const int n : row_tiles) {
     const int pieces = (n + T - 1) / T;
     most_pieces = pieces > most_pieces ? pieces : most_pieces;
     for (int i = 0; i < pieces; ++i) {
       const int size = (int)((int64_t)(i + 1) * n / pieces - (int64_t)i * n / pieces);
-      int best = 0;
-      for (int k = 1; k < c.slots; ++k) best = slot[k] < slot[best] ? k : best;
-      slot[best] += c.item_fixed + (size + c.parts - 1) / c.parts;
+      add_to_least(c.item_fixed + (size + c.parts - 1) / c.parts);
     }
   }
   int64_t makespan = 0;
-  for (int k = 0; k < c.slots; ++k) makespan = slot[k] > makespan ? slot[k] : makespan;
+  for (int k = 0; k < c.slots; ++k) makespan = heap[k] > makespan ? heap[k] : makespan;
   return makespan + (most_pieces > 1 ? c.merge_fixed + int64_t(c.merge_per_piece) * most_pieces : 0);
+}
+
+// Candidate T, largest first (see above); ladder_only keeps T <= kLadderTop.
+std::vector<int> split_candidates(int longest, int min_tiles, bool ladder_only) {
+  std::vector<int> t;
+  if (longest > kLadderTop && !ladder_only) {
+    for (int k = 1;; ++k) {
+      const int tk = (longest + k - 1) / k;
+      if (tk <= kLadderTop) break;
+      if (t.empty() || tk != t.back()) t.push_back(tk);
+    }
+  }
+  for (int tk = kLadderTop; tk >= min_tiles; tk -= kSplitStep) t.push_back(tk);
+  return t;
 }
 
 struct SplitChoice {
   int tiles_per_split;
-  int64_t makespan;  // in iterations; -1 when the simulation was skipped
+  int64_t makespan;  // in iterations; -1 when the simulation was skipped or no candidate fits
 };
 
 SplitChoice choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c,
-                                   int min_tiles = kMinSplitTiles) {
+                                   int min_tiles = kMinSplitTiles, bool ladder_only = false) {
   int64_t total = 0;
   int longest = 0;
   for (const int n : row_tiles) {
@@ -162,18 +234,27 @@ SplitChoice choose_tiles_per_split(const std::vector<int>& row_tiles, const Plan
     longest = n > longest ? n : longest;
   }
   if (longest <= min_tiles) return {min_tiles, simulated_makespan(row_tiles, min_tiles, c)};  // nothing to split
+  const std::vector<int> cands = split_candidates(longest, min_tiles, ladder_only);
   if (total / min_tiles > kMaxSimulatedItems) {
+    // Spread the tiles over one item per slot; the largest candidate that
+    // does not go below that and fits the workspace bound (one piece always
+    // does).  Such chunks have so many row blocks that this rarely splits.
     const int64_t per_item = (total + c.slots - 1) / c.slots;
-    return {(int)(per_item < min_tiles ? min_tiles : (per_item > tmx::kMaxItemTiles ? tmx::kMaxItemTiles : per_item)),
-            -1};
+    int pick = cands.front();
+    for (const int tk : cands) {
+      if (tk < per_item || !layout_fits(split_layout(row_tiles, tk))) break;
+      pick = tk;
+    }
+    return {pick, -1};
   }
-  int best_t = tmx::kMaxItemTiles;
-  int64_t best = simulated_makespan(row_tiles, best_t, c);
-  for (int t = tmx::kMaxItemTiles - kSplitStep; t >= min_tiles; t -= kSplitStep) {
-    const int64_t ms = simulated_makespan(row_tiles, t, c);
-    if (ms < best) {
+  int best_t = 0;
+  int64_t best = -1;
+  for (const int tk : cands) {
+    if (!layout_fits(split_layout(row_tiles, tk))) continue;
+    const int64_t ms = simulated_makespan(row_tiles, tk, c);
+    if (best < 0 || ms < best) {  // ties keep the larger T (fewer partials)
       best = ms;
-      best_t = t;
+      best_t = tk;
     }
   }
   return {best_t, best};
@@ -196,14 +277,22 @@ struct ChunkPlan {
 ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
   const int num_row_blocks = (int)row_tiles.size();
   if (num_row_blocks >= kHalvesMinRowBlocks) return {2, choose_tiles_per_split(row_tiles, kHalfCosts).tiles_per_split};
-  const SplitChoice quarters = choose_tiles_per_split(row_tiles, kQuarterCosts);
   if (sparse) {
     // TriangleMix: the shape whose best plan has the shorter makespan.
+    // Quarters take items of at most kLadderTop tiles here: with longer
+    // items the model, whose costs count a quarters iteration like a halves
+    // one although it moves twice the K/V, prefers quarters where halves
+    // measure faster (the last 512 rows of a 32768-token prompt: quarters
+    // over 256-tile items 92.1 us, halves over 147-tile items 85.6 us).
+    // Without a fitting quarters plan (rows too long for the workspace
+    // bound), halves run.
+    const SplitChoice quarters = choose_tiles_per_split(row_tiles, kQuarterCosts, kMinSplitTiles, true);
     const SplitChoice halves = choose_tiles_per_split(row_tiles, kHalfCosts, kFineSplitTiles);
     const bool use_halves = halves.makespan >= 0 && quarters.makespan >= 0 ? halves.makespan < quarters.makespan
                                                                            : quarters.makespan < 0;
     return use_halves ? ChunkPlan{2, halves.tiles_per_split} : ChunkPlan{4, quarters.tiles_per_split};
   }
+  const SplitChoice quarters = choose_tiles_per_split(row_tiles, kQuarterCosts);
   // Dense companion: halves when their plan splits a row block and the chunk
   // holds at least kHalvesDenseMinTiles tiles per KV head (the measured rule).
   const int t_halves = choose_tiles_per_split(row_tiles, kHalfCosts).tiles_per_split;
@@ -247,8 +336,8 @@ constexpr int64_t kMaxItemsPerHead = int64_t(1) << 26;
 struct Geometry {
   int sparse_begin, sparse_end, num_row_blocks, tiles_per_split, kv_parts;
   int64_t items_per_head;
-  bool any_split;
-  bool counters_fit;
+  int split_row_blocks;  // row blocks in issue order up to the last split one (0: nothing splits)
+  int64_t split_items;   // their items: the partial records per KV head
   int64_t workspace_bytes;
 };
 
@@ -260,23 +349,57 @@ Geometry make_geometry(bool sparse, int64_t query_tokens, int64_t query_start, i
   const ChunkPlan plan = cached_plan(PlanKey{g.num_row_blocks, query_start, seq_len, g.sparse_begin, g.sparse_end});
   g.kv_parts = plan.kv_parts;
   g.tiles_per_split = plan.tiles_per_split;
-  bool any_split = false;
   int64_t items = 0;
   for (int o = 0; o < g.num_row_blocks; ++o) {
     const int s = tmx::row_block_splits(o, g.num_row_blocks, (int)query_start, (int)seq_len, g.sparse_begin,
                                         g.sparse_end, g.tiles_per_split);
     items += s;
-    any_split = any_split || s > 1;
+    if (s > 1) {
+      g.split_row_blocks = o + 1;
+      g.split_items = items;
+    }
   }
   g.items_per_head = items;
-  g.any_split = any_split;
-  // The counter block holds the arrival counters of at most
-  // kMaxSplitRowBlocks row blocks; a larger chunk whose rows would split
-  // (rows of more than kMaxItemTiles tiles in a chunk of more than 32768
-  // tokens) is refused.
-  g.counters_fit = !any_split || g.num_row_blocks <= tmx::kMaxSplitRowBlocks;
-  g.workspace_bytes = any_split ? tmx::kCounterBytes + int64_t(tmx::kKvHeads) * items * tmx::kPartialBytes : 0;
+  g.workspace_bytes = g.split_row_blocks > 0
+                          ? tmx::kCounterBytes + int64_t(tmx::kKvHeads) * g.split_items * tmx::kPartialBytes
+                          : 0;
   return g;
+}
+
+// Validates a call's attributes and plans it: the launch, the workspace-size
+// queries and tm_chunk_plan share this, so a size query answers -1 for
+// exactly the calls a launch would refuse for their attributes.
+int plan_call(bool sparse, int64_t query_tokens, int64_t query_start, int64_t seq_len, int64_t prompt_len,
+              Geometry* g) {
+  const int st = check_attributes(query_tokens, query_start, seq_len, prompt_len, sparse);
+  if (st != TM_OK) return st;
+  *g = make_geometry(sparse, query_tokens, query_start, seq_len, prompt_len);
+  // The planner keeps every plan within these bounds; they guard the kernel's
+  // indexing should that ever change.
+  if (g->split_row_blocks > tmx::kMaxSplitRowBlocks || g->split_items > tmx::kMaxSplitItems ||
+      g->workspace_bytes > tmx::kMaxWorkspaceBytes) {
+    return fail(TM_ERR_UNSUPPORTED, "chunk plan needs %lld bytes of workspace; the limit is %lld",
+                (long long)g->workspace_bytes, (long long)tmx::kMaxWorkspaceBytes);
+  }
+  if (g->items_per_head > kMaxItemsPerHead) {
+    return fail(TM_ERR_UNSUPPORTED, "chunk needs %lld work items per KV head; the limit is %lld",
+                (long long)g->items_per_head, (long long)kMaxItemsPerHead);
+  }
+  return TM_OK;
+}
+
+// Arrival tag of one launch with split row blocks: nonzero and below 2^48,
+// different for every launch of the process (and, by its seed, unlikely to
+// meet another process's tags in a shared workspace).
+unsigned long long next_epoch() {
+  static std::atomic<unsigned long long> counter{[] {
+    const unsigned long long t = (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count();
+    return (t * 0x9E3779B97F4A7C15ull) ^ ((unsigned long long)getpid() << 24);
+  }()};
+  for (;;) {
+    const unsigned long long e = counter.fetch_add(1, std::memory_order_relaxed) & tmx::kEpochMask;
+    if (e != 0) return e;
+  }
 }
 
 int launch(bool sparse, const void* query, const void* key_cache, const void* value_cache,
@@ -316,20 +439,16 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
     return fail(TM_ERR_INVALID_ARGUMENT, "out must not overlap query, key_cache, value_cache or block_table");
   }
 
-  const Geometry g = make_geometry(sparse, query_tokens, query_start, seq_len, prompt_len);
-  if (!g.counters_fit) {
-    return fail(TM_ERR_UNSUPPORTED, "chunk of %d row blocks splits rows longer than %d keys; the limit is %d row blocks",
-                g.num_row_blocks, tmx::kMaxItemTiles * tmx::kKvTile, tmx::kMaxSplitRowBlocks);
-  }
-  if (g.items_per_head > kMaxItemsPerHead) {
-    return fail(TM_ERR_UNSUPPORTED, "chunk needs %lld work items per KV head; the limit is %lld",
-                (long long)g.items_per_head, (long long)kMaxItemsPerHead);
-  }
+  Geometry g;
+  st = plan_call(sparse, query_tokens, query_start, seq_len, prompt_len, &g);
+  if (st != TM_OK) return st;
   if (workspace_bytes < g.workspace_bytes) {
     return fail(TM_ERR_WORKSPACE, "workspace of %lld bytes is smaller than the %lld bytes this call needs",
                 (long long)workspace_bytes, (long long)g.workspace_bytes);
   }
   if (g.workspace_bytes > 0) {
+    // 64-bit atomics on the arrival words and 16-byte partial stores
+    if (((uintptr_t)workspace & 15) != 0) return fail(TM_ERR_WORKSPACE, "workspace must be 16-byte aligned");
     const Range r_ws{(uintptr_t)workspace, (uintptr_t)workspace + uintptr_t(g.workspace_bytes)};
     if (overlaps(r_ws, r_out) || overlaps(r_ws, r_q) || overlaps(r_ws, r_k) || overlaps(r_ws, r_v) ||
         overlaps(r_ws, r_bt)) {
@@ -343,8 +462,10 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   p.value_cache = static_cast<const __bf16*>(value_cache);
   p.block_table = block_table;
   p.out = static_cast<__bf16*>(out);
-  p.counters = g.any_split ? static_cast<unsigned*>(workspace) : nullptr;
-  p.partials = g.any_split ? reinterpret_cast<float*>(static_cast<char*>(workspace) + tmx::kCounterBytes) : nullptr;
+  const bool split = g.split_row_blocks > 0;
+  p.counters = split ? static_cast<unsigned long long*>(workspace) : nullptr;
+  p.partials = split ? reinterpret_cast<float*>(static_cast<char*>(workspace) + tmx::kCounterBytes) : nullptr;
+  p.epoch = split ? next_epoch() : 0;
   p.num_pages = (int)num_pages;
   p.query_start = (int)query_start;
   p.seq_len = (int)seq_len;
@@ -353,7 +474,8 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   p.num_row_blocks = g.num_row_blocks;
   p.tiles_per_split = g.tiles_per_split;
   p.items_per_head = (int)g.items_per_head;
-  p.any_split = g.any_split ? 1 : 0;
+  p.split_row_blocks = g.split_row_blocks;
+  p.split_items = (int)g.split_items;
   p.scale_log2 = scale * 1.4426950408889634f;
   const hipError_t err =
       tmx::launch_triangle_paged_attention(p, sparse, g.kv_parts, static_cast<hipStream_t>(stream));
@@ -394,8 +516,9 @@ int tm_triangle_paged_sparse_attention(const void* query, const void* key_cache,
 int64_t tm_triangle_paged_sparse_attention_workspace_size(int64_t query_tokens, int64_t query_start,
                                                           int64_t seq_len, int64_t prompt_len) {
   g_last_error[0] = '\0';
-  if (check_attributes(query_tokens, query_start, seq_len, prompt_len, true) != TM_OK) return -1;
-  return make_geometry(true, query_tokens, query_start, seq_len, prompt_len).workspace_bytes;
+  Geometry g;
+  if (plan_call(true, query_tokens, query_start, seq_len, prompt_len, &g) != TM_OK) return -1;
+  return g.workspace_bytes;
 }
 
 int tm_triangle_paged_sparse_attention_noalloc(const void* query, const void* key_cache, const void* value_cache,
@@ -404,10 +527,13 @@ int tm_triangle_paged_sparse_attention_noalloc(const void* query, const void* ke
                                                int64_t seq_len, int64_t prompt_len, float scale, void* stream) {
   g_last_error[0] = '\0';
   // Attributes first (same errors as the workspace entry point), then the
-  // scratch this geometry needs against what the per-GPU array holds.
-  const int st = check_attributes(query_tokens, query_start, seq_len, prompt_len, true);
+  // scratch this geometry needs against what the per-GPU array holds (the
+  // array is as large as any plan's workspace, so this guards a change of
+  // either bound).
+  Geometry g;
+  const int st = plan_call(true, query_tokens, query_start, seq_len, prompt_len, &g);
   if (st != TM_OK) return st;
-  const int64_t need = make_geometry(true, query_tokens, query_start, seq_len, prompt_len).workspace_bytes;
+  const int64_t need = g.workspace_bytes;
   if (need > tmx::kNoAllocScratchBytes) {
     return fail(TM_ERR_WORKSPACE,
                 "chunk needs %lld bytes of split-KV scratch; the no-allocation entry point holds %lld per GPU",
@@ -434,8 +560,9 @@ int tm_dense_paged_causal_attention(const void* query, const void* key_cache, co
 int64_t tm_dense_paged_causal_attention_workspace_size(int64_t query_tokens, int64_t query_start,
                                                        int64_t seq_len) {
   g_last_error[0] = '\0';
-  if (check_attributes(query_tokens, query_start, seq_len, seq_len, false) != TM_OK) return -1;
-  return make_geometry(false, query_tokens, query_start, seq_len, seq_len).workspace_bytes;
+  Geometry g;
+  if (plan_call(false, query_tokens, query_start, seq_len, seq_len, &g) != TM_OK) return -1;
+  return g.workspace_bytes;
 }
 
 int tm_chunk_plan(int dense, int64_t query_tokens, int64_t query_start, int64_t seq_len, int64_t prompt_len,
@@ -446,9 +573,9 @@ int tm_chunk_plan(int dense, int64_t query_tokens, int64_t query_start, int64_t 
   }
   const bool sparse = dense == 0;
   const int64_t prompt = sparse ? prompt_len : seq_len;
-  const int status = check_attributes(query_tokens, query_start, seq_len, prompt, sparse);
+  Geometry g;
+  const int status = plan_call(sparse, query_tokens, query_start, seq_len, prompt, &g);
   if (status != TM_OK) return status;
-  const Geometry g = make_geometry(sparse, query_tokens, query_start, seq_len, prompt);
   *kv_parts = g.kv_parts;
   *tiles_per_split = g.tiles_per_split;
   *items_per_kv_head = g.items_per_head;

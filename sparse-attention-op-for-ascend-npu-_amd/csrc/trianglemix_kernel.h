@@ -30,21 +30,32 @@ constexpr int kRowBlock = 32;  // query tokens per work item
 // row sum.
 constexpr int64_t kPartialFloats = int64_t(kGroup) * 64 * (64 + 2);
 constexpr int64_t kPartialBytes = kPartialFloats * 4;
-// Workspace of a launch with split row blocks: a block of arrival counters
-// (one per row block, KV head and workgroup position; zero before the launch,
-// and zero again when it completes), then the partials.  The counter block
-// has a fixed size so that it sits at the same place for every geometry: a
-// workspace zeroed once stays valid for any sequence of launches.
+// Workspace of a launch with split row blocks: a block of arrival words (one
+// 64-bit word per split row block, KV head and workgroup position), then the
+// partials of the split row blocks' items.  A word holds the launch's 48-bit
+// epoch above a 16-bit arrival count; a word carrying another epoch counts as
+// zero, so the workspace may hold anything before a launch (the reference's
+// workspace is plain scratch).  The workgroup that completes a row block
+// clears its word, so a graph that replays one launch (one epoch) finds it
+// clear again.  The counter block has a fixed size, so the partials start at
+// the same offset for every geometry.
 constexpr int64_t kCounterBytes = 65536;
-constexpr int kMaxSplitRowBlocks = int(kCounterBytes / 4 / (kKvHeads * 2));  // 1024
+constexpr int kMaxSplitRowBlocks = int(kCounterBytes / 8 / (kKvHeads * 2));  // 512
+constexpr int kEpochShift = 16;
+constexpr unsigned long long kEpochMask = (1ull << 48) - 1;
+// Largest workspace any call needs: the planner keeps every plan's counters
+// and partials within it (at most 124 split items per KV head), and a plan
+// with no split at all needs none.
+constexpr int64_t kMaxWorkspaceBytes = int64_t(64) << 20;
+constexpr int kMaxSplitItems = int((kMaxWorkspaceBytes - kCounterBytes) / (kKvHeads * kPartialBytes));  // 124
+static_assert(kMaxSplitItems < (1 << kEpochShift), "an arrival count fits below the epoch");
 // Split-KV scratch held per GPU for the no-allocation entry point (counter
-// block + partials): enough for every TriangleMix chunk of up to 2048 rows
-// at L <= 32768 and of up to 1024 rows at L <= 65536 (their splits need at
-// most 50 MB).
-constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
-// Largest number of tiles one work item may hold: the kernel keeps the item's
-// page numbers in two 64-lane registers.  Longer rows are split.
-constexpr int kMaxItemTiles = 128;
+// block + partials): the largest workspace of any call.
+constexpr int64_t kNoAllocScratchBytes = kMaxWorkspaceBytes;
+// A work item may hold any number of tiles: the kernel keeps the page numbers
+// of 128 of them in two 64-lane registers and refills the one it has used up
+// while the other serves, 64 tiles at a time.
+constexpr int kTableTiles = 64;
 // Most cache pages a launch accepts: the kernel addresses a key row of one KV
 // head by a 32-bit row index (page * 128 + slot) * 8 + head.  2^22 pages of
 // 256 KB per K or V cache are more than one GPU's memory.
@@ -94,8 +105,9 @@ struct KernelParams {
   const __bf16* value_cache;  // [num_pages, 128, 8, 128]
   const int32_t* block_table; // [>= ceil(seq_len/128)]
   __bf16* out;                // [tq, 32, 128]
-  float* partials;            // [8][items_per_head] split-KV partials, or null
-  unsigned* counters;         // [8][num_row_blocks][workgroups per item] arrival counters, or null
+  float* partials;            // [8][split_items] split-KV partials, or null
+  unsigned long long* counters;  // [8][split_row_blocks][workgroups per item] arrival words, or null
+  unsigned long long epoch;   // this launch's arrival tag: nonzero, below 2^48
   int num_pages;
   int query_start;
   int seq_len;
@@ -104,7 +116,12 @@ struct KernelParams {
   int num_row_blocks;
   int tiles_per_split; // max tiles per work item
   int items_per_head;  // sum over row blocks of their split counts
-  int any_split;       // 0: every row block is one item (item index = row-block order)
+  // The first split_row_blocks row blocks in issue order hold every split
+  // one (0 when none splits); their items, the first split_items, are
+  // decoded from the split counts.  Every later row block is one item:
+  // item split_items + j is row block split_row_blocks + j in issue order.
+  int split_row_blocks;
+  int split_items;
   float scale_log2;    // softmax scale * log2(e)
 };
 

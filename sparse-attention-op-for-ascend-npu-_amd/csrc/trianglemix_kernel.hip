@@ -17,8 +17,9 @@
 // merge through LDS at the end.  Two waves per SIMD let one wave's softmax
 // run while the other's MFMAs occupy the matrix core.
 // The KV tiles of a row block are cut into splits of at most
-// `tiles_per_split` tiles (host-chosen: at least 768 keys, at most
-// kMaxItemTiles tiles), so only long dense rows split.  A row block with one
+// `tiles_per_split` tiles (host-chosen for load balance: at least 768 keys,
+// no upper bound -- an item of any length runs in one workgroup), so only
+// long dense rows split.  A row block with one
 // split writes its output directly; otherwise every split writes an fp32
 // partial (O, row max, row sum) to the workspace and counts its arrival, and
 // the workgroup that arrives last merges all partials in split order
@@ -182,7 +183,9 @@ __device__ __forceinline__ int k_slot(int row, int chunk) { return chunk ^ (row 
 __device__ __forceinline__ int v_slot(int row, int chunk) { return chunk ^ ((row & 3) << 2); }
 
 // Work item -> (row-block order index, split index, split count), computed
-// by every wave from the row blocks' split counts (lane i: row block base + i).
+// by every wave from the split counts of the first p.split_row_blocks row
+// blocks in issue order (lane i: row block base + i), which hold items
+// 0 .. p.split_items - 1.
 // The exclusive prefix sum over the lanes needs no cross-lane data move: bit
 // by bit, it adds 2^b times the number of lower lanes whose count has bit b
 // set (v_mbcnt of a ballot).  That is a few VALU and SALU instructions per
@@ -194,9 +197,9 @@ __device__ __forceinline__ void decode_item(const KernelParams& p, int sparse_be
   order = 0;
   split = 0;
   nsplit = 1;
-  for (int base = 0; base < p.num_row_blocks; base += 64) {
+  for (int base = 0; base < p.split_row_blocks; base += 64) {
     const int o = base + lane;
-    const int cnt = o < p.num_row_blocks ? row_block_splits(o, p.num_row_blocks, p.query_start, p.seq_len,
+    const int cnt = o < p.split_row_blocks ? row_block_splits(o, p.num_row_blocks, p.query_start, p.seq_len,
                                                             sparse_begin, sparse_end, p.tiles_per_split)
                                          : 0;
     int excl = 0;   // items of the row blocks on lower lanes
@@ -337,7 +340,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   const int hp = (blockIdx.x / kKvHeads) % S::kWgPerKvHead;
   const int item = blockIdx.x / (kKvHeads * S::kWgPerKvHead);
   int order, split, nsplit;
-  if (p.any_split) {
+  if (item < p.split_items) {
     decode_item(p, sparse_begin, sparse_end, item, lane, order, split, nsplit);
     // The decoded item is wave-uniform; say so, so that all tile arithmetic,
     // block-table loads and buffer resources stay scalar.
@@ -345,7 +348,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     split = __builtin_amdgcn_readfirstlane(split);
     nsplit = __builtin_amdgcn_readfirstlane(nsplit);
   } else {
-    order = item;
+    order = p.split_row_blocks + (item - p.split_items);
     split = 0;
     nsplit = 1;
   }
@@ -361,7 +364,7 @@ triangle_paged_attention_kernel(KernelParams p) {
   // r = all % n: the first r splits get b + 1 tiles, the rest b.
   int t_lo = 0;
   int num_tiles = all_tiles;
-  if (p.any_split) {
+  if (nsplit > 1) {
     const int base = all_tiles / nsplit;
     const int rem = all_tiles - base * nsplit;
     t_lo = split * base + min(split, rem);
@@ -387,8 +390,11 @@ triangle_paged_attention_kernel(KernelParams p) {
     const int slot = dma_t == 0 ? k_slot(row, lane & 15) : v_slot(row, lane & 15);
     dma_voff[j] = (unsigned)(row * kKvHeads * kRowBytes + 16 * slot);
   }
-  // DMA source of every tile of the item (at most kMaxItemTiles = 128): lane
-  // i of row_lo holds tile i, lane i of row_hi tile 64 + i.  The value is the
+  // DMA source of the item's tiles, 64 at a time: table block b (tiles 64b ..
+  // 64b + 63) lives in row_lo when b is even and in row_hi when b is odd,
+  // tile 64b + i in lane i.  The prologue fills blocks 0 and 1; an item of
+  // more than 128 tiles refills a register in the loop once its block has
+  // been issued (see refill below).  The value is the
   // cache row index of the tile's first key row of this KV head (its byte
   // offset / 256, below 2^32 as the host caps the cache at kMaxPages pages);
   // bytes_lo / bytes_hi hold the tile's valid byte count (rows cut at seq_len,
@@ -410,7 +416,11 @@ triangle_paged_attention_kernel(KernelParams p) {
     return __builtin_amdgcn_raw_buffer_load_b32(bt_rsrc, off, 0, 0);
   };
   const int phys_lo = lane_page(lane);
-  const int phys_hi = lane_page(64 + lane);
+  const int phys_hi = lane_page(kTableTiles + lane);
+  // Table block 2, for an item of more than 128 tiles (for a shorter one the
+  // offset is out of range: the load returns 0 and touches no memory); the
+  // loop turns it into rows when block 0 is used up (refill below).
+  int refill_phys = lane_page(2 * kTableTiles + lane);
   // ---- Q: the workgroup's H heads x 32 rows (8 KB per head), DMA'd once into LDS ----
   // (each of the P part waves of a head needs all of it; loading it per wave
   // would multiply the start-up traffic through the CU).  Wave w loads the H
@@ -440,10 +450,10 @@ triangle_paged_attention_kernel(KernelParams p) {
     const int valid_rows = ti < num_tiles ? min(kKvTile, p.seq_len - lane_k0(ti)) : 0;
     return valid_rows > 0 ? (valid_rows - 1) * kKvHeads * kRowBytes + kRowBytes : 0;
   };
-  const unsigned row_lo = lane_row(lane, phys_lo);
-  const unsigned row_hi = lane_row(64 + lane, phys_hi);
-  const int bytes_lo = lane_bytes(lane);
-  const int bytes_hi = lane_bytes(64 + lane);
+  unsigned row_lo = lane_row(lane, phys_lo);
+  unsigned row_hi = lane_row(kTableTiles + lane, phys_hi);
+  int bytes_lo = lane_bytes(lane);
+  int bytes_hi = lane_bytes(kTableTiles + lane);
   // The tile tables are complete here, before any tile DMA: left to itself the
   // compiler sinks the part it needs only for tiles 64-127 into the loop's
   // preheader, and the wait for its block-table load there would also wait
@@ -455,8 +465,10 @@ triangle_paged_attention_kernel(KernelParams p) {
   // of this KV head, range cut at seq_len; a tile past the item's end gets an
   // empty range (its loads return zeros).
   auto tile_rsrc = [&](int ti, int t) {
-    const unsigned row = __builtin_amdgcn_readlane(ti < 64 ? row_lo : row_hi, ti & 63);
-    const int bytes = ti < num_tiles ? __builtin_amdgcn_readlane(ti < 64 ? bytes_lo : bytes_hi, ti & 63) : 0;
+    const unsigned u = (unsigned)ti;  // ti >= 0
+    const bool odd = ((u / kTableTiles) & 1) != 0;
+    const unsigned row = __builtin_amdgcn_readlane(odd ? row_hi : row_lo, u % kTableTiles);
+    const int bytes = ti < num_tiles ? __builtin_amdgcn_readlane(odd ? bytes_hi : bytes_lo, u % kTableTiles) : 0;
     const char* cache = reinterpret_cast<const char*>(t == 0 ? p.key_cache : p.value_cache);
     return __builtin_amdgcn_make_buffer_rsrc((void*)(cache + (size_t)row * kRowBytes), (short)0, bytes, kBufferFlags);
   };
@@ -597,6 +609,36 @@ triangle_paged_attention_kernel(KernelParams p) {
   m_run = m_tile;
   TM_PHASE(3);
 
+  // Table refill for items of more than 128 tiles.  Table block nb >= 2
+  // takes the register of block nb - 2.  The DMA of iteration it reaches
+  // tile P (it + 2) + P - 1 (K) and P (it + 1) + P - 1 (V), so block nb - 2
+  // is read for the last time in iteration 64 (nb - 1) / P - 2 and block nb
+  // first in iteration 64 nb / P - 2.  Right after the barrier that opens
+  // iteration 64 (nb - 1) / P - 1, before that iteration's DMA, block nb's
+  // pages (loaded 64 / P iterations earlier, in the prologue for block 2,
+  // and waited for by every iteration's wait for the wave's DMA since)
+  // become rows and byte counts, and block nb + 1's page loads are issued.
+  // One scalar compare per iteration; the refill itself is out of line.
+  int refill_it = num_tiles > 2 * kTableTiles ? kTableTiles / P - 1 : __INT_MAX__;
+  int refill_block = 2;
+  auto refill = [&](int it) {
+    if (__builtin_expect(it == refill_it, 0)) {
+      const int ti = kTableTiles * refill_block + lane;
+      const unsigned row = lane_row(ti, refill_phys);
+      const int bytes = lane_bytes(ti);
+      if (refill_block & 1) {
+        row_hi = row;
+        bytes_hi = bytes;
+      } else {
+        row_lo = row;
+        bytes_lo = bytes;
+      }
+      ++refill_block;
+      refill_phys = lane_page(kTableTiles * refill_block + lane);
+      refill_it += kTableTiles / P;
+    }
+  };
+
   // Iteration it (this wave's tile ti = 4*it + kq): state update with tile
   // ti's row max, then [QK^T of tile ti+4 (K slot kr) || exponentials of tile
   // ti], then [PV of tile ti (V slot vr) || mask and row max of tile ti+4];
@@ -615,6 +657,7 @@ triangle_paged_attention_kernel(KernelParams p) {
     } else {
       wait_dma();
       __syncthreads();  // DMA issued one iteration ago landed; slots kw / vw are no longer read
+      refill(it);
     }
     if (it < 8) TM_PHASE(4 + it);
     // The two waves of a SIMD (waves w and w + 4) leave the barrier
@@ -940,16 +983,17 @@ triangle_paged_attention_kernel(KernelParams p) {
   // heads, the parts disjoint d-blocks.  The records are written and read
   // with the sc1 cache policy (agent scope: stores written through to the
   // level where every L2 of the GPU is coherent, loads served from it), and
-  // the arrival counter is an agent-scope atomic, so no fence (a whole-L2
-  // writeback and invalidate) is needed.  Each wave waits for its own stores
-  // before the workgroup's arrival is counted; the workgroup that counts last
-  // has seen every other split arrive after their stores completed.
+  // the arrival word is updated by agent-scope atomics, so no fence (a
+  // whole-L2 writeback and invalidate) is needed.  Each wave waits for its
+  // own stores before the workgroup's arrival is counted; the workgroup that
+  // counts last has seen every other split arrive after their stores
+  // completed.
   constexpr int kStatM = kGroup * 64 * 64;     // row maxima [hq][lane]
   constexpr int kStatL = kGroup * 64 * 65;     // partial row sums [hq][lane]
   const int first = item - split;
   // Buffer over the row block's records (offsets stay 32-bit for any chunk).
   const __amdgpu_buffer_rsrc_t rec = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.partials + ((size_t)kvh * p.items_per_head + first) * kPartialFloats), (short)0,
+      (void*)(p.partials + ((size_t)kvh * p.split_items + first) * kPartialFloats), (short)0,
       nsplit * (int)kPartialBytes, kBufferFlags);
   // 16-byte piece g of d-block o: each instruction moves 64 lanes x 16 B = 1 KB contiguous.
   auto blk_off = [&](int s, int o, int g) {
@@ -974,16 +1018,35 @@ triangle_paged_attention_kernel(KernelParams p) {
   wait_dma();  // this wave's partial stores completed (vmcnt also counts stores)
   TM_PHASE(16);
   __syncthreads();
-  unsigned* ctr = p.counters + ((size_t)kvh * p.num_row_blocks + rb) * S::kWgPerKvHead + hp;
+  // Arrival word of (KV head, row block, workgroup position): this launch's
+  // epoch above the count of splits arrived under it.  A word that carries
+  // another epoch (left by another launch, cleared, or whatever the
+  // workspace held) counts as zero.  Each arrival adds one: when the word
+  // already carries this launch's epoch that is its count (one round trip,
+  // the case of every arrival after the first).  An arrival that finds
+  // another epoch has added to a void word; it then installs this launch's
+  // epoch with a count of one, or -- if another arrival installed it first
+  // -- adds itself under it, by compare-and-swap from the value last seen.
+  // Either way each arrival is counted exactly once under the epoch.
+  unsigned long long* ctr = p.counters + ((size_t)kvh * p.split_row_blocks + order) * S::kWgPerKvHead + hp;
   if (tid == 0) {
-    s_last = (int)(__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   (unsigned)(nsplit - 1));
+    const unsigned long long old = __hip_atomic_fetch_add(ctr, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long mine = old + 1;
+    if ((old >> kEpochShift) != p.epoch) {
+      unsigned long long seen = old + 1;  // the word if nobody else changed it since
+      do {
+        mine = (seen >> kEpochShift) == p.epoch ? seen + 1 : (p.epoch << kEpochShift) + 1;
+      } while (!__hip_atomic_compare_exchange_strong(ctr, &seen, mine, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+    }
+    s_last = (int)((mine & ((1ull << kEpochShift) - 1)) == (unsigned long long)nsplit);
   }
   __syncthreads();
   TM_PHASE(17);
   if (!s_last) return;
-  // Leave the counter zero for the next launch (every split has arrived).
-  if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Every split has arrived: clear the word, so that a replay of this very
+  // launch (same epoch, e.g. from a HIP graph) counts from zero again.
+  if (tid == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // One pass over the splits, kMergeBatch at a time with all of a batch's
   // loads in flight: a batch that raises the running max rescales what is

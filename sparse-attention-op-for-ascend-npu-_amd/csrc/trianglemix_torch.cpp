@@ -26,17 +26,17 @@
 // the same predicates and messages ("GPU" for "NPU").  Launches go on the
 // current HIP stream of the query's device under a device guard, with no
 // host synchronisation.  When the library reports a non-zero split-KV
-// workspace, it comes from a buffer kept per (device, stream) -- allocated
-// from PyTorch's caching allocator, as the reference's EXEC_NPU_CMD takes the
-// aclnn workspace from torch_npu's -- whose arrival counters are zeroed once
-// when it is created (the kernel leaves them zero).  Launches on one stream
-// run in order, so they share it.  A buffer, once handed out, stays alive
-// until the process ends (a larger one replaces it for later calls): a HIP
-// graph captured on a stream may keep using it on every replay.  Under
-// stream capture the stream's buffer is used when it is large enough;
-// otherwise the call gets a buffer of its own from the capture's memory, its
-// counters cleared by a captured fill.  A graph replayed on another stream
-// must not overlap other work on the capture stream's workspace.
+// workspace (at most TM_MAX_WORKSPACE_BYTES), it comes from PyTorch's caching
+// allocator, as the reference's EXEC_NPU_CMD takes the aclnn workspace from
+// torch_npu's.  Its contents do not matter (the library tags each arrival
+// word with its launch), so no buffer is ever cleared.  Outside stream
+// capture one buffer is kept per (device, stream) and shared by the launches
+// on that stream, which run in order; a call that needs more replaces it,
+// and the old buffer goes back to the caching allocator, which hands its
+// memory out again only in stream order.  Under stream capture every call
+// takes a buffer of its own from the capture's private pool, which the
+// graph keeps for its replays, so no graph depends on a buffer this file
+// may release.
 
 #include <ATen/ATen.h>
 #include <ATen/MemoryOverlap.h>
@@ -98,24 +98,17 @@ at::Tensor workspace_for(const at::Tensor& like, int64_t bytes, void* stream) {
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   TORCH_CHECK(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &capture) == hipSuccess,
               "hipStreamIsCapturing failed");
-  const bool capturing = capture != hipStreamCaptureStatusNone;
   const auto options = like.options().dtype(at::kByte);
+  if (capture != hipStreamCaptureStatusNone) return at::empty({bytes}, options);
   static std::mutex mutex;
-  // Every buffer ever handed out, per (device, stream); the last is current.
-  static std::map<std::pair<int, void*>, std::vector<at::Tensor>> cache;
+  static std::map<std::pair<int, void*>, at::Tensor> cache;  // the buffer of each (device, stream)
   std::lock_guard<std::mutex> lock(mutex);
-  std::vector<at::Tensor>& held = cache[{like.device().index(), stream}];
-  if (!held.empty() && held.back().numel() >= bytes) return held.back();
-  if (capturing) {
-    at::Tensor ws = at::empty({bytes}, options);
-    ws.narrow(0, 0, TM_WORKSPACE_COUNTER_BYTES).zero_();
-    return ws;
+  at::Tensor& held = cache[{like.device().index(), stream}];
+  if (!held.defined() || held.numel() < bytes) {
+    held = at::Tensor();  // released first, so that its memory may serve the larger buffer
+    held = at::empty({bytes}, options);
   }
-  const int64_t size = held.empty() ? bytes : std::max(bytes, 2 * held.back().numel());
-  at::Tensor ws = at::empty({size}, options);
-  ws.narrow(0, 0, TM_WORKSPACE_COUNTER_BYTES).zero_();
-  held.push_back(ws);
-  return ws;
+  return held;
 }
 
 void check_status(int status, const char* what) {

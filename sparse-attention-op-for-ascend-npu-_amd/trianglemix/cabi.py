@@ -62,13 +62,14 @@ def chunk_plan(query_tokens: int, query_start: int, seq_len: int, prompt_len: in
     return parts.value, tiles.value, items.value
 
 
-# Split-KV workspace per (device, stream): the first WORKSPACE_COUNTER_BYTES
-# are arrival counters that must be zero before a workspace's first use (the
-# kernel leaves them zero), so a buffer is zero-filled once when created and
-# then kept.  Every buffer handed out stays alive until the process ends (a
-# larger one replaces it for later calls), so work still queued on a stream,
-# or a graph captured on it, never sees its workspace freed.
+# Split-KV workspace per (device, stream), at most MAX_WORKSPACE_BYTES.  Its
+# contents before a call do not matter (the library tags every arrival word
+# with its launch), so a buffer is never cleared.  One buffer is kept per
+# (device, stream), allocated on that stream; a call that needs more replaces
+# it, and PyTorch's caching allocator hands the old buffer's memory out again
+# only in that stream's order, after the work queued on it.
 WORKSPACE_COUNTER_BYTES = 65536
+MAX_WORKSPACE_BYTES = 64 << 20
 _WORKSPACES: dict = {}
 
 
@@ -79,12 +80,13 @@ def _workspace(query, query_start, seq_len, prompt_len, workspace, stream):
     if workspace is None:
         import torch
 
-        held = _WORKSPACES.setdefault((query.device.index, int(stream)), [])
-        if not held or held[-1].numel() < need:
-            size = need if not held else max(need, 2 * held[-1].numel())
+        key = (query.device.index, int(stream))
+        held = _WORKSPACES.get(key)
+        if held is None or held.numel() < need:
+            _WORKSPACES.pop(key, None)
             with torch.cuda.stream(torch.cuda.ExternalStream(int(stream), device=query.device)):
-                held.append(torch.zeros(size, dtype=torch.uint8, device=query.device))
-        workspace = held[-1]
+                held = _WORKSPACES[key] = torch.empty(need, dtype=torch.uint8, device=query.device)
+        workspace = held
     return workspace.data_ptr(), workspace.numel() * workspace.element_size()
 
 

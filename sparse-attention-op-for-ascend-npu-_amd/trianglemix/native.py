@@ -23,7 +23,7 @@ PKG_DIR = Path(__file__).resolve().parent
 HIP_LIBRARY = PKG_DIR / "libtrianglemix.so"
 TORCH_ADAPTER = PKG_DIR / "_trianglemix_torch.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _LOCK = threading.Lock()
 _LOADED_ADAPTER_PATH: str | None = None

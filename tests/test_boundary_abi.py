@@ -7,8 +7,10 @@ No kernel runs here.  Checks:
 * every validation error of the launch entry points is returned before any
   HIP call (fake, never-dereferenced pointers; the attributes are invalid, so
   no launch is attempted);
-* the workspace-size entry points: zero when no row block is split, whole
-  per-item partial records otherwise, -1 on invalid attributes;
+* the workspace-size entry points: zero when no row block is split, the
+  arrival words plus whole partial records of the split row blocks' items
+  otherwise, never more than TM_MAX_WORKSPACE_BYTES, and -1 for exactly the
+  attributes the launch refuses;
 * the torch adapter registers the reference's exact schema strings
   (operator/torch_adapter/triangle_paged_attention_torch.cpp:264-296) plus the
   ``npu_triangle_paged_sparse_attention`` alias, shape-infers on the Meta
@@ -32,11 +34,12 @@ ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "trianglemix.h"
 KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 PARTIAL_BYTES = 4 * 64 * 66 * 4  # fp32 partial record of one (row block, kv head, split) item
-COUNTER_BYTES = 65536            # arrival counters at the front of a non-empty workspace (TM_WORKSPACE_COUNTER_BYTES)
+COUNTER_BYTES = 65536            # arrival words at the front of a non-empty workspace (TM_WORKSPACE_COUNTER_BYTES)
+MAX_WORKSPACE = 64 << 20         # TM_MAX_WORKSPACE_BYTES
 
 
 def _items(need: int) -> int:
-    """Work items per KV head a workspace size accounts for (0: no split, no workspace)."""
+    """Split items per KV head a workspace size accounts for (0: no split, no workspace)."""
     if need == 0:
         return 0
     assert need > COUNTER_BYTES and (need - COUNTER_BYTES) % (8 * PARTIAL_BYTES) == 0, need
@@ -85,6 +88,9 @@ def test_product_library_has_no_phase_clocks():
 def test_abi_version_and_status_strings(lib):
     m = re.search(r"#define\s+TM_ABI_VERSION\s+(\d+)", HEADER.read_text())
     assert lib.tm_abi_version() == int(m.group(1)) == native.ABI_VERSION
+    for name, value in (("TM_WORKSPACE_COUNTER_BYTES", COUNTER_BYTES), ("TM_MAX_WORKSPACE_BYTES", MAX_WORKSPACE)):
+        assert int(re.search(rf"#define\s+{name}\s+(\d+)", HEADER.read_text()).group(1)) == value
+    assert (cabi.WORKSPACE_COUNTER_BYTES, cabi.MAX_WORKSPACE_BYTES) == (COUNTER_BYTES, MAX_WORKSPACE)
     for code, name in [(0, "TM_OK"), (1, "TM_ERR_INVALID_ARGUMENT"), (2, "TM_ERR_UNSUPPORTED"),
                        (3, "TM_ERR_WORKSPACE"), (4, "TM_ERR_LAUNCH"), (99, "TM_ERR_UNKNOWN")]:
         assert lib.tm_status_string(code).decode() == name
@@ -136,6 +142,8 @@ def test_small_workspace_is_rejected_before_launch(lib):
     assert "smaller than" in lib.tm_last_error().decode()
     assert _sparse(lib, qs=7680, seq=8192, ws=OUT - 16, ws_bytes=need) == 3  # workspace overlapping out
     assert "overlap" in lib.tm_last_error().decode()
+    assert _sparse(lib, qs=7680, seq=8192, ws=WS + 8, ws_bytes=need) == 3  # 64-bit arrival words need alignment
+    assert "16-byte aligned" in lib.tm_last_error().decode()
 
 
 def test_dense_entry_validation_errors(lib):
@@ -178,17 +186,15 @@ def test_kv_write_without_tokens_enqueues_nothing(lib):
     assert _kv_write(lib, tokens=0, key=None, value=None, slots=None) == 0
 
 
-def test_noalloc_refuses_chunks_beyond_its_scratch_without_hip_calls(lib):
-    # fake (never dereferenced) pointers: both refusals happen before any HIP call
+def test_noalloc_refuses_what_the_workspace_entry_point_refuses(lib):
+    # fake (never dereferenced) pointers: the refusal happens before any HIP call
     fake = ctypes.c_void_p(0x1000)
-    # invalid attributes: the same error as the workspace entry point
     r = lib.tm_triangle_paged_sparse_attention_noalloc(fake, fake, fake, fake, fake, 512, 64, 64, 4096, 4000, 8192,
                                                        0.088, None)
     assert r == 1 and "Tq == seq_len" in lib.tm_last_error().decode()
-    # a dense 2048-row tail at L = 131072 needs ~100 MB of split scratch: more than the 64 MiB array
-    r = lib.tm_triangle_paged_sparse_attention_noalloc(fake, fake, fake, fake, fake, 2048, 1024, 1024, 129024,
-                                                       131072, 131072, 0.088, None)
-    assert r == 3 and "no-allocation" in lib.tm_last_error().decode()
+    # its 64 MiB array holds the largest workspace any chunk needs (the config-4 last chunk at L = 131072 needed
+    # ~100 MB when rows had to split every 4096 keys; it needs 17 MB now), so it accepts every valid chunk
+    assert 0 < lib.tm_triangle_paged_sparse_attention_workspace_size(2048, 129024, 131072, 131072) <= MAX_WORKSPACE
 
 
 def test_workspace_sizes(lib):
@@ -197,17 +203,71 @@ def test_workspace_sizes(lib):
     # sparse middle chunks: every row block holds few tiles -> no split, no workspace
     assert ws(512, 4096, 4608, 8192) == 0
     assert ws(5, 250, 255, 2048) == 0
-    # long rows (dense tail, dense companion) are split over KV -> whole partial records for 8 KV heads
+    # long rows (dense tail, dense companion) are split over KV when the chunk has too few row blocks to fill
+    # the GPU -> arrival words + whole partial records of the split items for 8 KV heads
     for n in (ws(512, 7680, 8192, 8192), dws(512, 7680, 8192)):
         assert n > 0 and _items(n) > 0
-    # a 2048-row chunk already fills the GPU with row blocks: no split ...
+    # a 2048-row chunk already fills the GPU with row blocks: no split, however long its rows (an item takes
+    # any number of tiles)
     assert dws(2048, 2048, 4096) == 0
-    # ... unless a row block holds more than 128 tiles (4096 keys), the most one item takes
-    assert dws(2048, 6272, 8320) > 0
+    assert dws(2048, 6272, 8320) == 0
+    assert dws(2048, 129024, 131072) == 0  # 1.1 GB when an item held at most 128 tiles
+    # only the split row blocks' items have partial records: the config-2 last chunk splits its 4 dense-tail
+    # row blocks in 3 (12 records), not its 12 sparse ones (24 items in all)
+    assert _items(ws(512, 7680, 8192, 8192)) == 12 and cabi.chunk_plan(512, 7680, 8192, 8192)[2] == 24
     # invalid attributes -> -1 with a message
     assert ws(0, 0, 0, 0) == -1 and lib.tm_last_error().decode()
     assert ws(512, 4096, 4608, 4000) == -1
     assert dws(512, 4000, 4608) == -1
+
+
+# (query_tokens, query_start, seq_len, prompt_len): chunks and whole prompts up to L = 131072, ragged and
+# mid-page, including every BASELINE configuration's chunks and whole-prompt calls of any length
+AGREE_GRID = sorted({
+    *[(c, s, s + c, L) for L in (2869, 8192, 8320, 32768, 40960, 131072) for c in (1, 32, 128, 512, 2048)
+      for s in (0, max(0, L - c - 4096), L - c) if s + c <= L],
+    *[(L, 0, L, L) for L in (1, 31, 521, 1000, 4096, 8320, 32768, 32769, 40960, 65536, 131072)],
+    (512, 2357, 2869, 2869), (100, 500, 600, 700), (300, 97, 397, 5000), (77, 8243, 8320, 8320),
+})
+
+
+def test_workspace_size_agrees_with_the_launch_over_a_grid(lib):
+    """For every geometry: the size query, the plan query and the launch accept or refuse alike; an accepted
+    call's workspace stays within TM_MAX_WORKSPACE_BYTES and holds the split items' partials; and a launch
+    given one byte less is refused for its workspace, while one given the full size passes the size check
+    (it then stops at an overlap check, so nothing is launched on these fake pointers)."""
+    parts, tiles, items = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    for tq, qs, seq, prompt in AGREE_GRID + [(512, 4000, 4608, 8192), (0, 0, 0, 0), (512, 4096, 4608, 4000)]:
+        for dense in (0, 1):
+            need = (lib.tm_dense_paged_causal_attention_workspace_size(tq, qs, seq) if dense
+                    else lib.tm_triangle_paged_sparse_attention_workspace_size(tq, qs, seq, prompt))
+            size_msg = lib.tm_last_error().decode()
+            plan = lib.tm_chunk_plan(dense, tq, qs, seq, prompt, ctypes.byref(parts), ctypes.byref(tiles),
+                                     ctypes.byref(items))
+            assert (need >= 0) == (plan == 0), (tq, qs, seq, prompt, dense)
+            pages = -(-max(seq, 1) // 128) + 1
+            a = dict(query=Q, key=K, value=V, table=BT, out=OUT, tq=tq, pages=pages, cols=pages, qs=qs, seq=seq,
+                     prompt=prompt, scale=0.0883883, ws=WS, ws_bytes=max(need - 1, 0))
+
+            def launch(**over):
+                b = dict(a, **over)
+                if dense:
+                    return lib.tm_dense_paged_causal_attention(b["query"], b["key"], b["value"], b["table"],
+                                                               b["out"], b["tq"], b["pages"], b["cols"], b["qs"],
+                                                               b["seq"], b["scale"], b["ws"], b["ws_bytes"], None)
+                return lib.tm_triangle_paged_sparse_attention(
+                    b["query"], b["key"], b["value"], b["table"], b["out"], b["tq"], b["pages"], b["cols"], b["qs"],
+                    b["seq"], b["prompt"], b["scale"], b["ws"], b["ws_bytes"], None)
+
+            if need < 0:
+                assert launch(ws=0, ws_bytes=0) == plan != 0
+                assert lib.tm_last_error().decode() == size_msg
+                continue
+            assert need <= MAX_WORKSPACE
+            assert _items(need) <= items.value and tiles.value >= 1 and parts.value in (2, 4)
+            if need > 0:
+                assert launch() == 3 and "smaller than" in lib.tm_last_error().decode()
+                assert launch(ws=OUT, ws_bytes=need) == 3 and "overlap" in lib.tm_last_error().decode()
 
 
 def test_cabi_workspace_size_wrapper(lib):
@@ -296,8 +356,9 @@ def _planned(lib, g):
     else:
         need = lib.tm_triangle_paged_sparse_attention_workspace_size(g["query_tokens"], g["query_start"],
                                                                      g["seq_len"], g["prompt_len"])
-    assert _items(need) in (0, items.value)  # the workspace holds one partial per item of a split plan
-    return parts.value, tiles.value, _items(need)
+    assert _items(need) <= items.value  # one partial per item of a split row block
+    # the sweep keys a plan by (KV parts, items per KV head), with 0 items for a plan that splits nothing
+    return parts.value, tiles.value, items.value if need > 0 else 0
 
 
 def _regret(lib, g):
@@ -334,6 +395,8 @@ BASELINE_PLANS = [
     ((6272, 2048, 8320, 8320), (2, 128, 72)),      # config 3
     ((8192, 128, 8320, 8320), (4, 84, 16)),        # config 3, last chunk
     ((30720, 2048, 32768, 32768), (2, 128, 92)),   # config 4, last chunk at L = 32768
+    ((129024, 2048, 131072, 131072), (2, 512, 92)),  # config 4, last chunk at L = 131072: tail rows in 8 pieces
+    ((0, 40960, 40960, 40960), (2, 1280, 1280)),   # a whole 40960-token prompt: one item per row block
 ]
 
 
@@ -371,16 +434,36 @@ def _items_at(T: int, qs: int, tq: int, seq: int, prompt: int | None) -> tuple[i
 
 def test_long_chunk_plan_skips_the_simulation_and_takes_the_largest_items(lib):
     """A chunk with more than 4096 candidate items (total tiles / 32, the smallest split) is not simulated:
-    its tiles spread over one item per slot, clamped to 128 tiles (csrc/trianglemix_capi.cpp
-    choose_tiles_per_split) -- for any such chunk that is 128 tiles, as total / 32 slots > 4096.
+    its tiles spread over one item per slot -- T is the smallest candidate of at least total / slots tiles
+    (csrc/trianglemix_capi.cpp choose_tiles_per_split), which for such a chunk is the longest row: no split.
     Pinned for the dense companion's last 2048-row chunk of a 131072-token prompt (64 row blocks of
-    4033-4096 tiles).  The TriangleMix chunk at the same place has 17458 tiles (sparse rows of 18 tiles,
-    four dense-tail rows of 4096) and stays below the bound: it is simulated."""
+    4033-4096 tiles): 64 items of whole rows, no workspace (2048 items and 1.1 GB of partials when an item
+    held at most 128 tiles).  The TriangleMix chunk at the same place has 17458 tiles (sparse rows of 18
+    tiles, four dense-tail rows of 4096) and stays below the bound: it is simulated, and splits its tail."""
     qs, tq, seq = 129024, 2048, 131072
-    total, items = _items_at(128, qs, tq, seq, None)
-    assert total // 32 > 4096 and -(-total // 32) > 128  # the shortcut applies, and it clamps
-    assert _items(lib.tm_dense_paged_causal_attention_workspace_size(tq, qs, seq)) == items == 64 * 32
-    # the item count tells T apart: one step of the candidate ladder (124 tiles) splits differently
-    assert _items_at(124, qs, tq, seq, None)[1] != items
+    total, items = _items_at(4096, qs, tq, seq, None)
+    assert total // 32 > 4096 and -(-total // 32) > 4096  # the shortcut applies: one slot's share > any row
+    assert cabi.chunk_plan(tq, qs, seq, None) == (2, 4096, 64) and items == 64
+    assert lib.tm_dense_paged_causal_attention_workspace_size(tq, qs, seq) == 0
     sparse_total, _ = _items_at(128, qs, tq, seq, 131072)
     assert sparse_total == 17458 and sparse_total // 32 <= 4096
+    assert cabi.chunk_plan(tq, qs, seq, 131072) == (2, 512, 92)  # four tail rows in 8 pieces + 60 sparse
+
+
+def test_whole_prompts_plan_without_refusal(lib):
+    """Whole-prompt calls (PrefillNoCache: query_start 0, Tq = seq_len = prompt_len) of any length are
+    accepted.  The dense companion plans one item per row block: a prompt has so many row blocks that no row
+    needs splitting.  The TriangleMix op splits at most its four dense-tail row blocks, where that balances
+    the slots (L = 65536: in two), within a few MB of workspace.  The planning stays cheap on the host even
+    at L = 131072 (4096 row blocks, simulated for the TriangleMix op)."""
+    import time
+    for L in (32769, 40960, 65536, 131072):
+        row_blocks = -(-L // 32)
+        for prompt in (L, None):
+            t0 = time.perf_counter()
+            parts, tiles, items = cabi.chunk_plan(L, 0, L, prompt)
+            assert time.perf_counter() - t0 < 0.1
+            assert parts == 2 and row_blocks <= items <= row_blocks + 4 * 8
+        assert cabi.chunk_plan(L, 0, L, None)[2] == row_blocks
+        assert lib.tm_dense_paged_causal_attention_workspace_size(L, 0, L) == 0
+        assert _items(cabi.workspace_size(L, 0, L, L)) <= 4 * 8

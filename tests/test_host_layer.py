@@ -298,3 +298,22 @@ def test_dispatch_reason_order():
         is FallbackReason.GRAPH_CAPTURE
     assert dispatch_reason(features=LayerFeatures(causal=False), capturing=False, native_ready=False, **common) \
         is FallbackReason.ADAPTER_UNAVAILABLE
+
+
+def test_whole_long_prompt_routes_direct():
+    """A whole-prompt PrefillNoCache step of 40960 tokens (planning.py:79-83 routes such steps direct) is planned
+    direct and launched on the direct path -- the op accepts a chunk of any length -- with no fallback."""
+    f = Fakes()
+    r, stats = _router(f)
+    L = 40960
+    plan = _plan(seq=L, qlen=L, prompt=L, state="PrefillNoCache")
+    assert plan.direct and plan.requests[0].query_len == L
+    q = torch.zeros(L, 32, 128, dtype=torch.bfloat16)
+    k = torch.zeros(L // 128 + 1, 128, 8, 128, dtype=torch.bfloat16)
+    bt = torch.zeros(1, L // 128 + 1, dtype=torch.int32)
+    r.prefill_attention(layer_name="model.layers.7.self_attn.attn", plan=plan, query=q, key_cache=k,
+                        value_cache=k.clone(), block_table=bt, output=torch.empty_like(q), softmax_scale=W.SCALE)
+    assert [c[0] for c in f.calls] == ["direct"]
+    assert stats.snapshot()["counters"]["layer_direct"] == 1
+    from trianglemix import cabi
+    assert cabi.workspace_size(L, 0, L, L) >= 0 and cabi.workspace_size(L, 0, L, None) == 0

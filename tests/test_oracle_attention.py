@@ -216,3 +216,64 @@ def test_planted_mistakes_fail(monkeypatch):
     sink = OA.joint_softmax_weighted_sum([0.0] * 8, [[10.0]] * 8)[0]
     local = OA.joint_softmax_weighted_sum([0.0] * 513, [[1.0]] * 513)[0]
     assert abs(sink + local - s["joint_expected"]) > s["tolerance"]
+
+
+# ---------------------------------------------------------------- the blocked restatement
+# ``attention_torch_blocked`` runs the same softmax for many rows at once (and on the GPU, where the long
+# whole-chunk parity tests use it).  Pinned here: its mask predicate against the set-builder form over every
+# row of several prompts, a planted off-by-one that this check catches, and its outputs against the per-row
+# fp32 oracle and the float64 one, with blocks forced small enough that every kind of block boundary occurs.
+
+@pytest.mark.parametrize("seq_len,prompt_len", [(700, 700), (1100, 5000), (1300, 1300), (650, 650), (520, 900)])
+def test_attended_mask_equals_set_builder(seq_len, prompt_len):
+    rows = torch.arange(0, seq_len)
+    keys = torch.arange(0, seq_len)
+    for dense in (False, True):
+        mask = OA.attended_mask(rows, keys, seq_len, prompt_len, dense=dense)
+        for q in range(seq_len):
+            want = list(range(q + 1)) if dense else _setbuilder(q, seq_len, prompt_len)
+            assert torch.nonzero(mask[q]).reshape(-1).tolist() == want, (q, dense)
+
+
+def test_attended_mask_planted_window_off_by_one_is_caught():
+    rows, keys = torch.arange(0, 1200), torch.arange(0, 1200)
+    good = OA.attended_mask(rows, keys, 1200, 1200)
+    q = rows.reshape(-1, 1)
+    k = keys.reshape(1, -1)
+    sparse = (q >= 521) & (q < 1200 - 128)
+    bad = (k <= q) & (~sparse | (k < 8) | (k >= q - 511))  # one window key dropped
+    assert not torch.equal(good, bad)
+    assert torch.nonzero(good[700]).reshape(-1).tolist() == _setbuilder(700, 1200, 1200)
+
+
+@pytest.mark.parametrize("qs,tq,seq,prompt,dense", [
+    (500, 100, 600, 700, False),     # dense prefix rows, the sparse start, sparse rows
+    (0, 700, 700, 700, False),       # a whole prompt: prefix, sparse middle, dense tail
+    (2357, 512, 2869, 2869, False),
+    (1000, 600, 1600, 5000, False),  # a prompt past the sequence: all sparse
+    (0, 300, 300, 300, True),        # dense companion, whole prompt
+    (1500, 233, 1733, 1733, True),   # dense companion, ragged chunk
+])
+def test_blocked_oracle_matches_per_row_oracles(qs, tq, seq, prompt, dense):
+    q, k, v, bt = make_inputs(qs, tq, seq, 77 + qs)
+    per_row = OA.attention_torch(q, k, v, bt, qs, seq, prompt, SCALE, dense=dense)
+    for max_scores in (1 << 14, 1 << 20, 1 << 26):  # blocks of 1-2 rows up to the whole chunk
+        blocked = OA.attention_torch_blocked(q, k, v, bt, qs, seq, prompt, SCALE, dense=dense,
+                                             max_scores=max_scores)
+        assert (blocked - per_row).abs().max().item() <= 4e-6, max_scores
+    if tq <= 400:  # the float64 restatement is slow; the per-row fp32 one above covers the larger chunks
+        ref64 = OA.attention_np(q.float().numpy(), k.float().numpy(), v.float().numpy(), bt.numpy(), qs, seq,
+                                prompt, SCALE, dense=dense)
+        assert np.abs(blocked.numpy() - ref64).max() <= 1e-4
+
+
+def test_blocked_oracle_zero_query_is_the_mean_of_selected_values():
+    qs, tq, seq, prompt = 400, 400, 800, 900
+    _, k, v, bt = make_inputs(qs, tq, seq, 5)
+    q = torch.zeros(tq, 32, 128, dtype=torch.bfloat16)
+    got = OA.attention_torch_blocked(q, k, v, bt, qs, seq, prompt, SCALE, max_scores=1 << 16)
+    lv = v[bt[0, :-(-seq // 128)].long()].reshape(-1, 8, 128)[:seq].double()
+    for r in (0, 120, 121, 122, 399):
+        keys = _setbuilder(qs + r, seq, prompt)
+        want = lv[keys].mean(0).repeat_interleave(4, dim=0)
+        assert torch.allclose(got[r].double(), want, atol=1e-5), r
