@@ -32,15 +32,17 @@ Reported JSON line (rank 0 only):
   (L=8320 in chunks of 2048, 1 % of K entries +-8, with max/mean-abs error vs
   the fp32 oracle on row subsets), config 4 (whole prefills at L=32768 and
   131072, chunk 2048, sparse vs dense) and config 5 (36 layers through the
-  plan / router layer, reference gates vs all dense, with the counters).
+  plan / router layer with the router's default gates on this GPU -- the
+  MI355X profile on gfx950 -- and with the reference's gates, vs all dense,
+  with the counters).
 
 ``--gpus N`` with N > 1 is refused: this build runs on one GPU.
 
 Detailed single-workload runs (one JSON line each, not the headline):
 ``--workload config1 | config3`` (same legs as the headline, that chunk set),
 ``--workload config4`` (the whole long-context curve, L = 1024 .. 131072, and
-the crossover), ``--workload config5`` (the layer stack with the MI355X
-gate profile, the structured counter log and the vLLM-ROCm seam).
+the crossover), ``--workload config5`` (the layer stack with both gate sets,
+the structured counter log and the vLLM-ROCm seam).
 """
 
 from __future__ import annotations
@@ -661,7 +663,9 @@ class LayerStack:
         self.chunks = prompt_chunks(self.L, self.CHUNK)
 
     def config(self, enabled: bool, profile: str = "", log_interval: int = 0):
-        from trianglemix.config import resolve_plugin_config
+        """The stack's plugin config: the gate profile measured on this GPU (the router's default), or the
+        named one ("reference": the reference's own gates)."""
+        from trianglemix.router import device_plugin_config
 
         section = {"enabled": enabled, "layers": self.SELECTED, "stats_log_interval": log_interval}
         if profile:
@@ -670,7 +674,7 @@ class LayerStack:
         class _Vllm:
             additional_config = {"trianglemix": section}
 
-        return resolve_plugin_config(_Vllm())
+        return device_plugin_config(_Vllm())
 
     def prefill(self, router, cfg) -> None:
         from trianglemix.planning import build_batch_plan
@@ -738,19 +742,30 @@ class LayerStack:
 
 
 def layer_stack_summary(seed: int) -> dict:
-    """Config 5 leg of the default run: reference gates vs every layer dense, with the counters."""
+    """Config 5 leg of the default run: the router's default gates (those measured on this GPU) and the
+    reference's gates vs every layer dense, with the counters."""
     import torch
 
+    from trianglemix.config import device_gate_profile
     from trianglemix.workload import chunk_flops
 
     stack = LayerStack(seed)
-    res = stack.run((("trianglemix", True, "", 0), ("all_dense", False, "", 0)))
+    res = stack.run((("trianglemix", True, "", 0), ("reference_gates", True, "reference", 0),
+                     ("all_dense", False, "", 0)))
     sel = stack.config(True).kernel.layer_indices
     tm = res["trianglemix"]["stats"]
+    ref = res["reference_gates"]
     out = {
         "workload": f"L={stack.L}, chunked prefill {stack.CHUNK} x {len(stack.chunks)}, {stack.LAYERS} layers, "
-                    f"layers {stack.SELECTED} sparse, reference gates; eager, median of 3 interleaved prefills",
+                    f"layers {stack.SELECTED} sparse; eager, median of 3 interleaved prefills",
+        "gates": device_gate_profile() or "reference",
         "ms_per_prefill": res["trianglemix"]["ms_per_prefill"],
+        "reference_gates": {
+            "ms_per_prefill": ref["ms_per_prefill"],
+            "attention_time_cut": round(1 - ref["ms_per_prefill"] / res["all_dense"]["ms_per_prefill"], 4),
+            "counters": {k: v for k, v in ref["stats"]["counters"].items() if not k.endswith("_ns")},
+            "fallback_reasons": ref["stats"]["fallback_reasons"],
+        },
         "all_dense_ms_per_prefill": res["all_dense"]["ms_per_prefill"],
         "attention_time_cut": round(1 - res["trianglemix"]["ms_per_prefill"] / res["all_dense"]["ms_per_prefill"], 4),
         "gflop": {"routed": round(sum(chunk_flops(c, dense=(i not in sel)) for c in stack.chunks
@@ -774,9 +789,8 @@ def host_overhead(args) -> int:
     import torch
 
     from trianglemix import cabi, kernel, native
-    from trianglemix.config import resolve_plugin_config
     from trianglemix.planning import build_batch_plan
-    from trianglemix.router import TriangleMixRouter
+    from trianglemix.router import TriangleMixRouter, device_plugin_config
     from trianglemix.stats import TriangleMixRuntimeStats
     from trianglemix.workload import SCALE, make_cache, make_query
 
@@ -795,7 +809,7 @@ def host_overhead(args) -> int:
         class _Vllm:
             additional_config = {"trianglemix": {"enabled": True, "layers": layers}}
 
-        cfg = resolve_plugin_config(_Vllm())
+        cfg = device_plugin_config(_Vllm())
         return cfg, TriangleMixRouter(cfg, stats=TriangleMixRuntimeStats())
 
     cfg, router = router_for("0-35")
@@ -854,6 +868,7 @@ def host_overhead(args) -> int:
 def config5_stack(args) -> int:
     """36 layers x config 2 through the plan / router layer; counters from the stats snapshot."""
     from trianglemix import native
+    from trianglemix.config import device_gate_profile
     from trianglemix.counters import aggregate as counters_aggregate
     from trianglemix.counters import report_status, scan_events
     from trianglemix.workload import chunk_flops
@@ -863,7 +878,7 @@ def config5_stack(args) -> int:
     stack = LayerStack(args.seed)
     chunks, L, layers = stack.chunks, stack.L, stack.LAYERS
     results = stack.run((("trianglemix", True, "", 0),
-                         ("trianglemix_mi355x_gates", True, "mi355x", 0),
+                         ("trianglemix_reference_gates", True, "reference", 0),
                          ("all_dense", False, "", 0),
                          ("trianglemix_logged", True, "", len(chunks))), windows=1)
     # the structured log of the logged run, aggregated the way a run's worker logs are
@@ -891,14 +906,15 @@ def config5_stack(args) -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 Q/K/V per layer from the GPU generator, random page table)",
         "config": {"workload": f"config5: L={L}, chunked prefill {stack.CHUNK} x {len(chunks)}, {layers} layers, "
-                               f"layers {stack.SELECTED} sparse", "gates": "reference defaults"},
+                               f"layers {stack.SELECTED} sparse",
+                   "gates": (device_gate_profile() or "reference") + " (the router's default on this GPU)"},
         "all_dense_ms_per_prefill": results["all_dense"]["ms_per_prefill"],
-        "mi355x_gates": {
-            "ms_per_prefill": results["trianglemix_mi355x_gates"]["ms_per_prefill"],
-            "attention_time_cut": round(1 - results["trianglemix_mi355x_gates"]["ms_per_prefill"]
+        "reference_gates": {
+            "ms_per_prefill": results["trianglemix_reference_gates"]["ms_per_prefill"],
+            "attention_time_cut": round(1 - results["trianglemix_reference_gates"]["ms_per_prefill"]
                                         / results["all_dense"]["ms_per_prefill"], 4),
-            "counters": results["trianglemix_mi355x_gates"]["stats"]["counters"],
-            "fallback_reasons": results["trianglemix_mi355x_gates"]["stats"]["fallback_reasons"],
+            "counters": results["trianglemix_reference_gates"]["stats"]["counters"],
+            "fallback_reasons": results["trianglemix_reference_gates"]["stats"]["fallback_reasons"],
         },
         "attention_time_cut": round(1 - results["trianglemix"]["ms_per_prefill"]
                                     / results["all_dense"]["ms_per_prefill"], 4),

@@ -8,7 +8,8 @@ Outputs (next to the Python package, git-ignored, shipped with the tree):
 
 Usage: ``python build.py [--hip-only]``.  Each call recompiles.
 ``python build.py --phase-clocks`` builds the diagnostic phase-clock library
-``trianglemix/libtrianglemix_phase_clocks.so`` instead (see trianglemix/phase_clocks.py).
+``trianglemix/libtrianglemix_phase_clocks.so`` instead: a diagnostic build whose kernels store
+per-wave ``s_memrealtime`` clocks at phase boundaries (exports ``tm_phase_clocks_read`` / ``_clear``).
 """
 
 from __future__ import annotations
@@ -70,7 +71,7 @@ def _atomic_replace(tmp: Path, dst: Path) -> None:
 
 def build_hip_library(phase_clocks: bool = False) -> Path:
     """The kernels + C ABI; ``phase_clocks`` builds the diagnostic variant that records per-wave phase clocks
-    (trianglemix/phase_clocks.py reads them) into its own file."""
+    (read back through its ``tm_phase_clocks_read`` export) into its own file."""
     hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
     dst = PHASE_CLOCK_LIB if phase_clocks else HIP_LIB
     tmp = dst.with_suffix(".so.tmp")

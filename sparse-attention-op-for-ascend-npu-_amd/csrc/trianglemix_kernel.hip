@@ -118,8 +118,8 @@ constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 
 // Phase clocks (diagnostic builds only, -DTRIANGLEMIX_PHASE_CLOCKS): lane 0 of
-// every wave stores the 100 MHz s_memrealtime clock at the phases listed in
-// trianglemix/phase_clocks.py, one 64-bit slot per (workgroup, wave, phase),
+// every wave stores the 100 MHz s_memrealtime clock at the TM_PHASE(slot)
+// points below, one 64-bit slot per (workgroup, wave, phase),
 // for grids of up to kPhaseClockWorkgroups workgroups.  The product library
 // is built without them.
 #ifdef TRIANGLEMIX_PHASE_CLOCKS

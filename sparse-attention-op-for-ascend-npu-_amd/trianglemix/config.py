@@ -16,9 +16,13 @@ several bad values the first row's error is the one raised.
 One key is this build's own: ``gate_profile`` (environment
 ``VLLM_ASCEND_TRIANGLE_MIX_GATE_PROFILE``) names a crossover profile measured
 by ``trianglemix.calibrate`` -- a name under ``trianglemix/gate_profiles/``
-(``"mi355x"`` ships) or a JSON path.  Its gates replace the defaults of the
-five ``direct_*`` gate keys; explicit keys and environment variables still
-win.  Unset, the reference's 910B-measured defaults apply unchanged.
+(``"mi355x"`` ships) or a JSON path; ``"reference"`` names the reference's
+own gates.  Its gates replace the defaults of the five ``direct_*`` gate
+keys; explicit keys and environment variables still win.  Unset,
+``resolve_plugin_config`` takes its ``default_gate_profile`` argument, whose
+default keeps the reference's 910B-measured gates; the engine seam and
+``router.device_plugin_config`` pass ``device_gate_profile()``, the profile
+measured on the GPU they run on (``"mi355x"`` on gfx950).
 """
 
 from __future__ import annotations
@@ -146,11 +150,34 @@ def load_gate_profile(name_or_path: str) -> dict[str, int]:
     return {f: int(gates[f]) for f in _GATE_FIELDS}
 
 
-def resolve_plugin_config(vllm_config: object | None) -> PluginConfig:
-    """Resolve the typed configuration, preferring ``additional_config.trianglemix``."""
+# GPU architecture -> the gate profile measured on it.
+_DEVICE_PROFILES = {"gfx950": "mi355x"}
+REFERENCE_PROFILE = "reference"  # the reference's own (910B-measured) gates
+
+
+def device_gate_profile(device: object | None = None) -> str:
+    """The gate profile measured on the GPU ``device`` (default: the current one), or "" when none was."""
+    try:
+        import torch
+
+        if not torch.cuda.is_available():
+            return ""
+        arch = torch.cuda.get_device_properties(device if device is not None else torch.cuda.current_device())
+        name = str(getattr(arch, "gcnArchName", "")).split(":")[0]
+    except Exception:
+        return ""
+    return _DEVICE_PROFILES.get(name, "")
+
+
+def resolve_plugin_config(vllm_config: object | None, *, default_gate_profile: str = "") -> PluginConfig:
+    """Resolve the typed configuration, preferring ``additional_config.trianglemix``.
+
+    ``default_gate_profile`` applies when neither the section nor the
+    environment names a ``gate_profile``; by default the reference's gates.
+    """
     source = _Source(vllm_config)
-    profile = str(source.get(_GATE_PROFILE) or "")
-    profile_gates = load_gate_profile(profile) if profile else {}
+    profile = str(source.get(_GATE_PROFILE, default_gate_profile or None) or "").strip()
+    profile_gates = load_gate_profile(profile) if profile and profile != REFERENCE_PROFILE else {}
     kernel = TriangleMixConfig(**{s.field: source.get(s, profile_gates.get(s.field)) for s in _KERNEL_SETTINGS})
     recent, interval = source.get(_RECENT_CAPACITY), source.get(_LOG_INTERVAL)
     if recent < 0 or interval < 0:

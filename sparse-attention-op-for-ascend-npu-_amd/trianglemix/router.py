@@ -25,7 +25,7 @@ import time
 from dataclasses import dataclass
 from typing import Any, Callable
 
-from .config import PluginConfig
+from .config import PluginConfig, device_gate_profile, resolve_plugin_config
 from .counters import log_if_due
 from .kernel import (
     SUPPORTED_CACHE_BLOCK_SIZE,
@@ -206,6 +206,13 @@ def dispatch_reason(*, config: PluginConfig, plan: TriangleBatchPlan, features: 
         if reason is not FallbackReason.NONE:
             return reason
     return _block_table_reason(block_table, query, plan.requests[0].seq_len)
+
+
+def device_plugin_config(vllm_config: object | None, device: object | None = None) -> PluginConfig:
+    """``resolve_plugin_config`` with the plan gates measured on the GPU this process runs on (the
+    ``mi355x`` profile on gfx950: every chunk with a sparse middle goes direct) unless the configuration or
+    the environment names a ``gate_profile`` (``"reference"`` keeps the reference's 910B gates)."""
+    return resolve_plugin_config(vllm_config, default_gate_profile=device_gate_profile(device))
 
 
 class TriangleMixRouter:

@@ -56,10 +56,10 @@ from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Any, Callable
 
-from .config import PluginConfig, resolve_plugin_config
+from .config import PluginConfig
 from .kernel import TriangleMixConfig
 from .planning import TriangleBatchPlan, build_batch_plan
-from .router import LayerFeatures, TriangleMixRouter, leading_rows
+from .router import LayerFeatures, TriangleMixRouter, device_plugin_config, leading_rows
 from .stats import runtime_stats
 
 logger = logging.getLogger("vllm.trianglemix.rocm")
@@ -272,7 +272,7 @@ def config_of(owner: object) -> PluginConfig:
         return cached
     vllm_config = getattr(owner, "vllm_config", None) or _current_vllm_config()
     try:
-        config = resolve_plugin_config(vllm_config)
+        config = device_plugin_config(vllm_config)
     except Exception:
         runtime_stats().record_runtime_error(stage="config")
         if _strict_env():

@@ -107,3 +107,37 @@ def test_without_profile_reference_defaults_stay(monkeypatch):
 def test_unknown_profile_is_an_error():
     with pytest.raises(ValueError, match="not found"):
         resolve_plugin_config(_VllmConfig({"gate_profile": "no_such_gpu"}))
+
+
+def test_device_default_profile_and_reference_opt_out(monkeypatch):
+    """The engine seam and ``router.device_plugin_config`` default to the profile measured on the GPU they run
+    on; ``resolve_plugin_config`` alone keeps the reference's gates.  A configured or environment profile wins
+    over the device default, and ``"reference"`` names the reference's own gates."""
+    from trianglemix import config as C
+    from trianglemix import router as R
+
+    monkeypatch.delenv("VLLM_ASCEND_TRIANGLE_MIX_GATE_PROFILE", raising=False)
+    gates = load_gate_profile("mi355x")
+    dev = resolve_plugin_config(_VllmConfig({}), default_gate_profile="mi355x").kernel
+    assert all(getattr(dev, f) == v for f, v in gates.items())
+    ref = resolve_plugin_config(_VllmConfig({"gate_profile": "reference"}), default_gate_profile="mi355x").kernel
+    assert (ref.direct_min_saved_qk, ref.direct_split_min_saved_qk) == (913_152, 1_299_264)
+    monkeypatch.setenv("VLLM_ASCEND_TRIANGLE_MIX_GATE_PROFILE", "reference")
+    env = resolve_plugin_config(_VllmConfig({}), default_gate_profile="mi355x").kernel
+    assert env.direct_min_saved_qk == 913_152
+    monkeypatch.delenv("VLLM_ASCEND_TRIANGLE_MIX_GATE_PROFILE")
+    # the device lookup: gfx950 -> mi355x; no GPU (this container) -> none, so the reference gates
+    assert C._DEVICE_PROFILES["gfx950"] == "mi355x" and (GATE_PROFILE_DIR / "mi355x.json").is_file()
+    monkeypatch.setattr(C, "device_gate_profile", lambda device=None: "mi355x")
+    monkeypatch.setattr(R, "device_gate_profile", lambda device=None: "mi355x")
+    assert R.device_plugin_config(_VllmConfig({})).kernel.direct_min_saved_qk == gates["direct_min_saved_qk"]
+    monkeypatch.setattr(R, "device_gate_profile", lambda device=None: "")
+    assert R.device_plugin_config(_VllmConfig({})).kernel.direct_min_saved_qk == 913_152
+
+
+def test_device_gate_profile_without_a_gpu():
+    import torch
+
+    from trianglemix.config import device_gate_profile
+    if not torch.cuda.is_available():
+        assert device_gate_profile() == ""

@@ -89,3 +89,19 @@ def test_fast_gates_equal_generic_gates(gpu):
     bad = R.LayerFeatures(num_heads=16)
     assert R.dispatch_reason(config=config, plan=plan, features=bad, capturing=False, native_ready=True,
                              **base) is _generic(bad, plan, **base) is FallbackReason.QUERY_UNSUPPORTED
+
+
+def test_gfx950_takes_the_mi355x_gate_profile_by_default(gpu):
+    """On gfx950 the seam's and the router helper's configuration carry the MI355X gates (all 0: every chunk
+    with a sparse middle goes direct), while ``resolve_plugin_config`` alone keeps the reference's."""
+    from trianglemix.config import device_gate_profile, load_gate_profile, resolve_plugin_config
+    from trianglemix.router import device_plugin_config
+
+    class _V:
+        additional_config = {"trianglemix": {"enabled": True, "layers": "5"}}
+
+    assert device_gate_profile() == "mi355x"
+    cfg = device_plugin_config(_V()).kernel
+    for field, value in load_gate_profile("mi355x").items():
+        assert getattr(cfg, field) == value
+    assert resolve_plugin_config(_V()).kernel.direct_min_saved_qk == 913_152
