@@ -43,6 +43,7 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime.h>
+#include <torch/extension.h>
 #include <torch/library.h>
 
 #include <map>
@@ -263,7 +264,83 @@ at::Tensor& meta_dense_out(const at::Tensor&, const at::Tensor&, const at::Tenso
   return output;
 }
 
+// ---- routed-call fast path (the Python module trianglemix._trianglemix_torch) ----
+// The routing layer pays its tensor gates and the op call on every selected
+// layer of every step, and an eager prefill waits for that host time.  These
+// entry points give it the same gates in one native call and the .out
+// launches without the dispatcher's Python argument handling; the launches
+// run the ops' own checks, device guard and workspace code above.
+
+// First failing tensor gate of a routed call whose query is on a GPU: 0 none,
+// 1 query / output, 2 KV cache, 3 block table.  The predicates and their order
+// are the routing layer's (trianglemix/router.py, _tensor_reason), which
+// restate the reference plugin's _validate_query / _validate_static_kv /
+// _validate_block_table (package/src/vllm_ascend_trianglemix/plugin.py:1106-1192).
+int64_t tensor_gate(const at::Tensor& query, const at::Tensor& output, const at::Tensor& key_cache,
+                    const at::Tensor& value_cache, const at::Tensor& block_table, int64_t query_len,
+                    int64_t seq_len) {
+  constexpr auto kBf16 = at::ScalarType::BFloat16;
+  if (query.dim() != 3 || query.size(1) != 32 || query.size(2) != 128 || query.size(0) != query_len ||
+      query.scalar_type() != kBf16 || !query.is_contiguous()) {
+    return 1;
+  }
+  const auto device = query.get_device();
+  if (output.dim() == 0 || output.size(0) < query.size(0) || output.scalar_type() != kBf16 ||
+      output.get_device() != device || !output.is_contiguous()) {
+    return 1;
+  }
+  if (key_cache.dim() != 4 || key_cache.size(1) != 128 || key_cache.size(2) != 8 || key_cache.size(3) != 128 ||
+      value_cache.sizes() != key_cache.sizes() || key_cache.scalar_type() != kBf16 ||
+      value_cache.scalar_type() != kBf16 || key_cache.get_device() != device || value_cache.get_device() != device ||
+      !key_cache.is_contiguous() || !value_cache.is_contiguous()) {
+    return 2;
+  }
+  if (block_table.dim() != 2 || block_table.size(0) != 1 || block_table.size(1) < (seq_len + 127) / 128 ||
+      block_table.scalar_type() != at::ScalarType::Int || block_table.get_device() != device ||
+      !block_table.is_contiguous()) {
+    return 3;
+  }
+  return 0;
+}
+
+// The routed launches: rows [seq_len - Tq, seq_len) into the first Tq rows of
+// `output` (an engine's output buffer may hold padding rows past them).
+void launch_sparse(const at::Tensor& query, const at::Tensor& key_cache, const at::Tensor& value_cache,
+                   const at::Tensor& block_table, int64_t seq_len, int64_t prompt_len, double scale,
+                   const at::Tensor& output) {
+  const int64_t rows = query.size(0);
+  at::Tensor out = output.size(0) == rows ? output : output.narrow(0, 0, rows);
+  triangle_paged_sparse_attention_out(query, key_cache, value_cache, block_table, seq_len - rows, seq_len, prompt_len,
+                                      scale, out);
+}
+
+// tensor_gate, then -- when every gate passes (result 0) -- launch_sparse: one
+// native call for a routed direct layer whose engine runs nothing between the
+// gates and the launch.
+int64_t route_sparse(const at::Tensor& query, const at::Tensor& output, const at::Tensor& key_cache,
+                     const at::Tensor& value_cache, const at::Tensor& block_table, int64_t query_len, int64_t seq_len,
+                     int64_t prompt_len, double scale) {
+  const int64_t gate = tensor_gate(query, output, key_cache, value_cache, block_table, query_len, seq_len);
+  if (gate == 0) launch_sparse(query, key_cache, value_cache, block_table, seq_len, prompt_len, scale, output);
+  return gate;
+}
+
+void launch_dense(const at::Tensor& query, const at::Tensor& key_cache, const at::Tensor& value_cache,
+                  const at::Tensor& block_table, int64_t seq_len, double scale, const at::Tensor& output) {
+  const int64_t rows = query.size(0);
+  at::Tensor out = output.size(0) == rows ? output : output.narrow(0, 0, rows);
+  dense_paged_causal_attention_out(query, key_cache, value_cache, block_table, seq_len - rows, seq_len, scale, out);
+}
+
 }  // namespace trianglemix_rocm
+
+PYBIND11_MODULE(_trianglemix_torch, m) {
+  m.doc() = "Routed-call fast path of the TriangleMix torch adapter (the ops themselves are under torch.ops)";
+  m.def("tensor_gate", &trianglemix_rocm::tensor_gate);
+  m.def("launch_sparse", &trianglemix_rocm::launch_sparse);
+  m.def("route_sparse", &trianglemix_rocm::route_sparse);
+  m.def("launch_dense", &trianglemix_rocm::launch_dense);
+}
 
 TORCH_LIBRARY(trianglemix_reference, ops) {
   ops.def(

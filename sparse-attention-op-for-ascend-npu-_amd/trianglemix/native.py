@@ -169,3 +169,31 @@ def require_adapter() -> None:
         status = ensure_native_loaded(strict=False)
         if not status.ready:
             raise NativeUnavailable(f"TriangleMix native adapter unavailable: {status.reason}")
+
+
+_ROUTED = None  # the adapter's routed-call module once imported, False when it cannot be
+
+
+def routed_fast_path():
+    """The torch adapter's routed-call entry points (``tensor_gate``, ``launch_sparse``, ``launch_dense``),
+    or None.
+
+    The adapter library is also a Python extension module: for the routing
+    layer it gives the per-call tensor gates in one native call and the
+    ``.out`` launches without the dispatcher's Python argument handling.  It
+    is imported only once the adapter is loaded from this package's own file
+    (importing another file would register the ops a second time).
+    """
+    global _ROUTED
+    if _ROUTED is None:
+        with _LOCK:
+            own = _LOADED_ADAPTER_PATH is not None and _LOADED_ADAPTER_PATH == _normalise(TORCH_ADAPTER)
+        if not own:
+            return None
+        try:
+            import importlib
+
+            _ROUTED = importlib.import_module(__package__ + "._trianglemix_torch")
+        except ImportError:
+            _ROUTED = False
+    return _ROUTED or None

@@ -9,6 +9,7 @@ of the reference pin the behaviour (tests/test_policy_golden.py).
 
 from __future__ import annotations
 
+import functools
 import itertools
 import time
 from dataclasses import dataclass
@@ -60,8 +61,9 @@ class TriangleRequestPlan:
     def query_len(self) -> int:
         return self.q_end - self.q_begin
 
-    @property
+    @functools.cached_property
     def saved_qk(self) -> int:
+        # cached: the routing layer reads it on every direct layer call of the plan
         return 0 if self.span is None else self.span.saved_qk
 
 

@@ -36,7 +36,7 @@ from .kernel import (
     extract_layer_index,
     triangle_direct_after_gates,
 )
-from .native import triangle_mix_adapter_loaded
+from .native import routed_fast_path, triangle_mix_adapter_loaded
 from .planning import FallbackReason, TriangleBatchPlan
 from .stats import TriangleMixRuntimeStats, runtime_stats
 
@@ -183,25 +183,54 @@ def _tensor_reason(features: LayerFeatures, query, output, key_cache, value_cach
     return FallbackReason.NONE
 
 
-def dispatch_reason(*, config: PluginConfig, plan: TriangleBatchPlan, features: LayerFeatures, query: object,
-                    output: object, key_cache: object, value_cache: object, block_table: object,
-                    capturing: bool, native_ready: bool) -> FallbackReason:
-    """First failing gate for a selected layer, or ``FallbackReason.NONE``."""
+def _all_gpu_tensors(query, output, key_cache, value_cache, block_table) -> bool:
+    tensor = _torch_types()[0]
+    return (type(query) is tensor and type(output) is tensor and type(key_cache) is tensor
+            and type(value_cache) is tensor and type(block_table) is tensor and query.is_cuda)
+
+
+# tensor_gate's result codes (csrc/trianglemix_torch.cpp)
+_GATE_CODES = (FallbackReason.NONE, FallbackReason.QUERY_UNSUPPORTED, FallbackReason.KV_CACHE_UNSUPPORTED,
+               FallbackReason.BLOCK_TABLE_UNSUPPORTED)
+
+
+def _call_reason(config: PluginConfig, plan: TriangleBatchPlan, features: LayerFeatures, capturing: bool,
+                 native_ready: bool) -> FallbackReason:
+    """The gates before the tensor gates: capture, the planner, the adapter, the model."""
     if capturing:
         return FallbackReason.GRAPH_CAPTURE
     if not plan.direct:
         return plan.primary_reason
     if not native_ready:
         return FallbackReason.ADAPTER_UNAVAILABLE
-    reason = _model_reason(features, config)
+    return _model_reason(features, config)
+
+
+def _head_counts_supported(features: LayerFeatures) -> bool:
+    return (features.num_heads == SUPPORTED_QUERY_HEADS and features.num_kv_heads == SUPPORTED_KV_HEADS
+            and features.head_size == SUPPORTED_HEAD_SIZE)
+
+
+def dispatch_reason(*, config: PluginConfig, plan: TriangleBatchPlan, features: LayerFeatures, query: object,
+                    output: object, key_cache: object, value_cache: object, block_table: object,
+                    capturing: bool, native_ready: bool) -> FallbackReason:
+    """First failing gate for a selected layer, or ``FallbackReason.NONE``."""
+    reason = _call_reason(config, plan, features, capturing, native_ready)
     if reason is not FallbackReason.NONE:
         return reason
     tensor = _torch_types()[0]
     if (type(query) is tensor and type(output) is tensor and type(key_cache) is tensor
             and type(value_cache) is tensor and type(block_table) is tensor and query.is_cuda):
         request = plan.requests[0]
-        return _tensor_reason(features, query, output, key_cache, value_cache, block_table, request.query_len,
-                              request.seq_len)
+        fast = routed_fast_path()
+        if fast is None:
+            return _tensor_reason(features, query, output, key_cache, value_cache, block_table, request.query_len,
+                                  request.seq_len)
+        # the same gates in one native call (the adapter's tensor_gate); the layer's head counts stay here
+        if not _head_counts_supported(features):
+            return FallbackReason.QUERY_UNSUPPORTED
+        return _GATE_CODES[fast.tensor_gate(query, output, key_cache, value_cache, block_table, request.query_len,
+                                            request.seq_len)]
     for reason in (_query_reason(features, query, output, plan), _kv_reason(key_cache, value_cache, query)):
         if reason is not FallbackReason.NONE:
             return reason
@@ -233,14 +262,43 @@ class TriangleMixRouter:
         self._direct = direct_fn
         self._dense = dense_fn
         self._native_ready = native_ready
+        # With the default ops, GPU tensors launch through the adapter's routed-call entry points.
+        self._native_direct = direct_fn is triangle_direct_after_gates
+        self._native_dense = dense_fn is dense_paged_causal_attention
+        self._layers: dict[str, tuple[bool, int | None]] = {}  # layer name -> (selected, layer index)
+        self._ready = False  # the adapter was seen loaded (it stays loaded)
+
+    def _layer(self, layer_name: str) -> tuple[bool, int | None]:
+        known = self._layers.get(layer_name)
+        if known is None:
+            known = (self.config.kernel.uses_layer(layer_name), extract_layer_index(layer_name))
+            if len(self._layers) < 4096:
+                self._layers[layer_name] = known
+        return known
 
     def _dense_fallback(self, *, query, key_cache, value_cache, block_table, seq_len: int, output, scale: float):
+        if self._native_dense and type(query) is _torch_types()[0] and query.is_cuda:
+            fast = routed_fast_path()
+            if fast is not None:
+                fast.launch_dense(query, key_cache, value_cache, block_table, seq_len, scale, output)
+                return output
         view = output[: query.shape[0]]
         return self._dense(query=query, key_cache=key_cache, value_cache=value_cache, block_table=block_table,
                            seq_len=seq_len, output=view, softmax_scale=scale)
 
     def _log_if_due(self) -> None:
         log_if_due(self.stats, logger)
+
+    def _launch_failed(self, plan: TriangleBatchPlan, layer_index: int | None, layer_name: str,
+                       dense: Callable[[], Any]):
+        """A failing direct launch (called from its ``except``): counted, raised in strict mode, else the
+        fallback path."""
+        self.stats.record_runtime_error(stage="direct_launch")
+        if self.config.strict:
+            raise
+        logger.exception("TriangleMix direct launch failed at layer %s; using the fallback path", layer_name)
+        self._count_fallback(plan, layer_index, FallbackReason.DIRECT_LAUNCH_ERROR)
+        return dense()
 
     def _count_fallback(self, plan: TriangleBatchPlan, layer_index: int | None, reason: FallbackReason) -> None:
         # Graph-capture metadata is a reusable dummy, not a scheduled request.
@@ -272,35 +330,58 @@ class TriangleMixRouter:
                                         block_table=block_table, output=output, scale=softmax_scale,
                                         seq_len=plan.requests[0].seq_len)
 
-        if not self.config.enabled or plan is None or not self.config.kernel.uses_layer(layer_name):
+        if not self.config.enabled or plan is None:
             return dense()
-        layer_index = extract_layer_index(layer_name)
-        reason = dispatch_reason(config=self.config, plan=plan, features=features, query=query, output=output,
-                                 key_cache=key_cache, value_cache=value_cache, block_table=block_table,
-                                 capturing=capturing, native_ready=self._native_ready())
+        selected, layer_index = self._layer(layer_name)
+        if not selected:
+            return dense()
+        if not self._ready:
+            self._ready = bool(self._native_ready())
+        request = plan.requests[0]
+        reason = _call_reason(self.config, plan, features, capturing, self._ready)
+        if (reason is FallbackReason.NONE and before_direct is None and self._native_direct
+                and _head_counts_supported(features) and _all_gpu_tensors(query, output, key_cache, value_cache,
+                                                                          block_table)):
+            fast = routed_fast_path()
+            if fast is not None:
+                # the tensor gates and, when they pass, the launch in one native call
+                started = time.perf_counter_ns()
+                try:
+                    code = fast.route_sparse(query, output, key_cache, value_cache, block_table, request.query_len,
+                                             request.seq_len, request.prompt_len, float(softmax_scale))
+                except Exception:
+                    return self._launch_failed(plan, layer_index, layer_name, dense)
+                if code:
+                    self._count_fallback(plan, layer_index, _GATE_CODES[code])
+                    return dense()
+                self.stats.record_direct_launch(plan, layer_index=layer_index,
+                                                host_enqueue_ns=time.perf_counter_ns() - started)
+                self._log_if_due()
+                return output
+        if reason is FallbackReason.NONE:
+            reason = dispatch_reason(config=self.config, plan=plan, features=features, query=query, output=output,
+                                     key_cache=key_cache, value_cache=value_cache, block_table=block_table,
+                                     capturing=capturing, native_ready=self._ready)
         if reason is not FallbackReason.NONE:
             self._count_fallback(plan, layer_index, reason)
             return dense()
-        request = plan.requests[0]
         rows = request.query_len
         started = time.perf_counter_ns()
         try:
             if before_direct is not None:
                 before_direct()
-            self._direct(query=leading_rows(query, rows), key_cache=key_cache, value_cache=value_cache,
-                         block_table=block_table, seq_len=request.seq_len, prompt_len=request.prompt_len,
-                         output=leading_rows(output, rows),
-                         softmax_scale=float(softmax_scale), config=self.config.kernel)
+            fast = routed_fast_path() if self._native_direct and query.is_cuda else None
+            if fast is not None:  # the gates passed: five torch tensors on the query's GPU, query of `rows` rows
+                fast.launch_sparse(query, key_cache, value_cache, block_table, request.seq_len, request.prompt_len,
+                                   float(softmax_scale), output)
+            else:
+                self._direct(query=leading_rows(query, rows), key_cache=key_cache, value_cache=value_cache,
+                             block_table=block_table, seq_len=request.seq_len, prompt_len=request.prompt_len,
+                             output=leading_rows(output, rows),
+                             softmax_scale=float(softmax_scale), config=self.config.kernel)
         except Exception:
-            self.stats.record_runtime_error(stage="direct_launch")
-            if self.config.strict:
-                raise
-            logger.exception("TriangleMix direct launch failed at layer %s; using the fallback path", layer_name)
-            self._count_fallback(plan, layer_index, FallbackReason.DIRECT_LAUNCH_ERROR)
-            return dense()
+            return self._launch_failed(plan, layer_index, layer_name, dense)
         enqueue_ns = time.perf_counter_ns() - started
-        self.stats.record_planner_decision(plan)
-        self.stats.record_layer_dispatch(plan_id=plan.plan_id, layer_index=layer_index, saved_qk=request.saved_qk,
-                                         host_enqueue_ns=enqueue_ns, request_index=request.request_index)
+        self.stats.record_direct_launch(plan, layer_index=layer_index, host_enqueue_ns=enqueue_ns)
         self._log_if_due()
         return output

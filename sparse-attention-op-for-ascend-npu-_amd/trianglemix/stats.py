@@ -230,6 +230,11 @@ class _LogCadence:
         return boundary, deltas
 
 
+# layer index -> its counter key, str(layer index) (the routing layer records one per call)
+_LAYER_KEYS: dict = {}
+_NONE_REASON = FallbackReason.NONE.value
+
+
 class _Tallies:
     def __init__(self) -> None:
         self.counters: Counter[str] = Counter()
@@ -287,42 +292,65 @@ class TriangleMixRuntimeStats:
         not a user request (``batch_size`` is 0) and is not counted.
         """
         with self._lock:
-            if plan.plan_id in self._seen:
-                return
-            self._seen[plan.plan_id] = None
-            if len(self._seen) > SEEN_PLAN_WINDOW:
-                self._seen.popitem(last=False)
-            counted = plan.requests[:plan.batch_size]
-            ineligible = [r for r in counted if not r.eligible]
-            c = self._tallies.counters
-            c["routing_ns"] += plan.routing_ns
-            c["request_total"] += plan.batch_size
-            c["request_planner_eligible"] += plan.batch_size - len(ineligible)
-            c["request_planner_ineligible"] += len(ineligible)
-            self._tallies.reasons.update(r.reason.value for r in ineligible)
-            if self._log.interval:
-                self._buffer_locked({
-                    "kind": "planner", "plan_id": plan.plan_id, "state": plan.state_name,
-                    "batch_size": plan.batch_size, "route": _plan_route(plan), "reason": plan.primary_reason.value,
-                    "requests": [{"slot": r.request_index, "eligible": r.eligible, "reason": r.reason.value}
-                                 for r in counted],
-                })
-                self._log.plan_counted(plan.plan_id, c["request_total"])
-            self._trace.add(plan, counted)
+            self._count_plan_locked(plan)
+
+    def _count_plan_locked(self, plan: TriangleBatchPlan) -> None:
+        if plan.plan_id in self._seen:
+            return
+        self._seen[plan.plan_id] = None
+        if len(self._seen) > SEEN_PLAN_WINDOW:
+            self._seen.popitem(last=False)
+        counted = plan.requests[:plan.batch_size]
+        ineligible = [r for r in counted if not r.eligible]
+        c = self._tallies.counters
+        c["routing_ns"] += plan.routing_ns
+        c["request_total"] += plan.batch_size
+        c["request_planner_eligible"] += plan.batch_size - len(ineligible)
+        c["request_planner_ineligible"] += len(ineligible)
+        self._tallies.reasons.update(r.reason.value for r in ineligible)
+        if self._log.interval:
+            self._buffer_locked({
+                "kind": "planner", "plan_id": plan.plan_id, "state": plan.state_name,
+                "batch_size": plan.batch_size, "route": _plan_route(plan), "reason": plan.primary_reason.value,
+                "requests": [{"slot": r.request_index, "eligible": r.eligible, "reason": r.reason.value}
+                             for r in counted],
+            })
+            self._log.plan_counted(plan.plan_id, c["request_total"])
+        self._trace.add(plan, counted)
 
     def record_layer_dispatch(self, *, plan_id: int, layer_index: int | None, saved_qk: int,
                               host_enqueue_ns: int, request_index: int = 0) -> None:
         """A selected layer ran the sparse kernel (one launch)."""
         with self._lock:
-            c = self._tallies.counters
-            c["layer_direct"] += 1
-            c["single_launch"] += 1
-            c["estimated_saved_qk"] += saved_qk
-            c["host_enqueue_ns"] += host_enqueue_ns
-            c["host_enqueue_ns_max"] = max(c["host_enqueue_ns_max"], host_enqueue_ns)
-            self._tallies.direct_layers[str(layer_index)] += 1
-            self._layer_event_locked(plan_id, _LayerEvent(layer_index, "direct", FallbackReason.NONE.value,
-                                                          (request_index,), 1, saved_qk, host_enqueue_ns))
+            self._dispatch_locked(plan_id, layer_index, saved_qk, host_enqueue_ns, request_index)
+
+    def record_direct_launch(self, plan: TriangleBatchPlan, *, layer_index: int | None,
+                             host_enqueue_ns: int) -> None:
+        """``record_planner_decision(plan)`` then ``record_layer_dispatch`` of the plan's first request,
+        under one lock: what the routing layer records for every direct layer call."""
+        request = plan.requests[0]
+        with self._lock:
+            self._count_plan_locked(plan)
+            self._dispatch_locked(plan.plan_id, layer_index, request.saved_qk, host_enqueue_ns,
+                                  request.request_index)
+
+    def _dispatch_locked(self, plan_id: int, layer_index: int | None, saved_qk: int, host_enqueue_ns: int,
+                         request_index: int) -> None:
+        c = self._tallies.counters
+        c["layer_direct"] += 1
+        c["single_launch"] += 1
+        c["estimated_saved_qk"] += saved_qk
+        c["host_enqueue_ns"] += host_enqueue_ns
+        if host_enqueue_ns > c["host_enqueue_ns_max"]:
+            c["host_enqueue_ns_max"] = host_enqueue_ns
+        key = _LAYER_KEYS.get(layer_index)
+        if key is None:
+            key = str(layer_index)
+            if len(_LAYER_KEYS) < 4096:
+                _LAYER_KEYS[layer_index] = key
+        self._tallies.direct_layers[key] += 1
+        self._layer_event_locked(plan_id, _LayerEvent(layer_index, "direct", _NONE_REASON, (request_index,), 1,
+                                                      saved_qk, host_enqueue_ns))
 
     def record_layer_fallback(self, *, plan_id: int | None = None, layer_index: int | None,
                               reason: FallbackReason, request_indices: tuple[int, ...] = ()) -> None:

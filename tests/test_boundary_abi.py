@@ -470,3 +470,36 @@ def test_whole_prompts_plan_without_refusal(lib):
         assert cabi.chunk_plan(L, 0, L, None)[2] == row_blocks
         assert lib.tm_dense_paged_causal_attention_workspace_size(L, 0, L) == 0
         assert _items(cabi.workspace_size(L, 0, L, L)) <= 4 * 8
+
+
+def test_routed_fast_path_gate_equals_the_python_gates(adapter):
+    """The adapter library is also the Python module of the routed-call fast path.  Its ``tensor_gate`` names
+    the same first failing gate as the router's Python ``_tensor_reason`` for a well-formed call and one broken
+    property at a time (CPU tensors here: the gates compare devices with each other, so everything but a
+    device mismatch is covered; tests/test_gpu_router_gates.py covers those on the GPU)."""
+    from trianglemix import router as R
+
+    fast = native.routed_fast_path()
+    assert fast is not None and {"tensor_gate", "launch_sparse", "launch_dense"} <= set(dir(fast))
+    tq, seq = 64, 700
+    bf = torch.bfloat16
+    base = dict(query=torch.zeros(tq, 32, 128, dtype=bf), output=torch.zeros(tq + 3, 32, 128, dtype=bf),
+                key_cache=torch.zeros(7, 128, 8, 128, dtype=bf), value_cache=torch.zeros(7, 128, 8, 128, dtype=bf),
+                block_table=torch.zeros(1, 6, dtype=torch.int32))
+    cases = [{}, {"query": base["query"].half()}, {"query": torch.zeros(tq + 1, 32, 128, dtype=bf)},
+             {"query": torch.zeros(tq, 32, 256, dtype=bf)[:, :, :128]}, {"query": torch.zeros(tq, 4096, dtype=bf)},
+             {"output": torch.zeros(tq - 1, 32, 128, dtype=bf)}, {"output": torch.zeros((), dtype=bf)},
+             {"output": torch.zeros(tq, 32, 128)}, {"key_cache": torch.zeros(7, 64, 8, 128, dtype=bf)},
+             {"value_cache": torch.zeros(8, 128, 8, 128, dtype=bf)}, {"value_cache": base["value_cache"].half()},
+             {"key_cache": torch.zeros(7, 128, 16, 128, dtype=bf)[:, :, ::2]},
+             {"block_table": torch.zeros(1, 5, dtype=torch.int32)}, {"block_table": torch.zeros(1, 6, dtype=torch.int64)},
+             {"block_table": torch.zeros(2, 6, dtype=torch.int32)},
+             {"block_table": torch.zeros(1, 12, dtype=torch.int32)[:, ::2]}]
+    seen = set()
+    for change in cases:
+        t = {**base, **change}
+        args = (t["query"], t["output"], t["key_cache"], t["value_cache"], t["block_table"])
+        py = R._tensor_reason(R.LayerFeatures(), *args, tq, seq)
+        assert R._GATE_CODES[fast.tensor_gate(*args, tq, seq)] is py, (change.keys(), py)
+        seen.add(py)
+    assert len(seen) == 4  # every reason reached, and the well-formed call passes

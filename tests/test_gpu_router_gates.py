@@ -1,13 +1,14 @@
-"""The router's gates on GPU tensors: the fast path equals the generic predicates.
+"""The router's gates on GPU tensors: the fast paths equal the generic predicates.
 
-``router.dispatch_reason`` reads torch tensors whose query is on a GPU
-through ``_tensor_reason`` (direct attribute reads, device indices) and
-everything else through ``_query_reason`` / ``_kv_reason`` /
+``router.dispatch_reason`` checks torch tensors whose query is on a GPU in
+one native call (the adapter's ``tensor_gate``; ``_tensor_reason`` is the
+same gates in Python, for an adapter without that module) and everything
+else through ``_query_reason`` / ``_kv_reason`` /
 ``_block_table_reason`` (the restatement of the reference's
 ``_validate_query`` / ``_validate_static_kv`` / ``_validate_block_table``,
 plugin.py:1106-1192).  For a well-formed call and for one broken property at
 a time -- dtype, shape, row count, contiguity, device, block-table length --
-both must name the same reason.
+all three must name the same reason.
 """
 
 from __future__ import annotations
@@ -75,12 +76,22 @@ def test_fast_gates_equal_generic_gates(gpu):
     assert plan.direct
     features = R.LayerFeatures()
     seen = set()
+    from trianglemix.native import routed_fast_path
+
+    fast = routed_fast_path()
+    assert fast is not None  # the adapter's routed-call module (dispatch_reason's gate on GPU tensors)
     for name, change in cases:
         t = {**base, **change}
         want = _generic(features, plan, **t)
         got = R.dispatch_reason(config=config, plan=plan, features=features, capturing=False, native_ready=True,
                                 **t)
         assert got is want, (name, got, want)
+        # the Python restatement of the same gates agrees with the native one
+        py = R._tensor_reason(features, t["query"], t["output"], t["key_cache"], t["value_cache"],
+                              t["block_table"], tq, seq)
+        native = R._GATE_CODES[fast.tensor_gate(t["query"], t["output"], t["key_cache"], t["value_cache"],
+                                                t["block_table"], tq, seq)]
+        assert py is native is want, (name, py, native, want)
         seen.add(want)
     # the cases reach every tensor reason and the well-formed call passes
     assert seen == {FallbackReason.NONE, FallbackReason.QUERY_UNSUPPORTED, FallbackReason.KV_CACHE_UNSUPPORTED,
@@ -105,3 +116,47 @@ def test_gfx950_takes_the_mi355x_gate_profile_by_default(gpu):
     for field, value in load_gate_profile("mi355x").items():
         assert getattr(cfg, field) == value
     assert resolve_plugin_config(_V()).kernel.direct_min_saved_qk == 913_152
+
+
+def test_router_native_paths(gpu):
+    """The routing layer's native paths with the real ops: a routed direct call (gates and launch in one native
+    call) is bit-identical to the op called directly, writes only the query's rows of a padded output, and
+    counts one launch; a call that fails a tensor gate there (a strided block table) counts that reason and
+    runs the engine's fallback; a call with an engine hook between the gates and the launch (before_direct)
+    takes the two-step path, runs the hook once, and gives the same bits."""
+    from trianglemix.router import TriangleMixRouter
+    from trianglemix.stats import TriangleMixRuntimeStats
+    from trianglemix.workload import SCALE, make_cache, make_query
+
+    tq, seq, prompt = 512, 4608, 8192
+    k, v, bt = make_cache(seq, 21, std=1.0)
+    qd, kd, vd, btd = make_query(tq, 22, std=1.0).to(gpu), k.to(gpu), v.to(gpu), bt.to(gpu)
+    kcfg = TriangleMixConfig(enabled=True, layer_indices=frozenset({5}))
+    plan = build_batch_plan(state_name="ChunkedPrefill", cumulative_query_ends=[tq], seq_lens=[seq],
+                            prompt_lens=[prompt], num_decodes=0, num_prefills=1, config=kcfg)
+    stats = TriangleMixRuntimeStats()
+    router = TriangleMixRouter(PluginConfig(kernel=kcfg), stats=stats)
+    want = torch.empty_like(qd)
+    torch.ops.trianglemix.triangle_paged_sparse_attention.out(qd, kd, vd, btd, seq - tq, seq, prompt, SCALE, out=want)
+    layer = "model.layers.5.self_attn.attn"
+    print("router native paths: routed direct call", flush=True)
+    padded = torch.full((tq + 8, 32, 128), float("nan"), dtype=torch.bfloat16, device=gpu)
+    router.prefill_attention(layer_name=layer, plan=plan, query=qd, key_cache=kd, value_cache=vd, block_table=btd,
+                             output=padded, softmax_scale=SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(padded[:tq], want) and torch.isnan(padded[tq:].float()).all()
+    strided = torch.zeros(1, 2 * btd.shape[1], dtype=torch.int32, device=gpu)
+    strided[:, ::2] = btd
+    fell_back = []
+    router.prefill_attention(layer_name=layer, plan=plan, query=qd, key_cache=kd, value_cache=vd,
+                             block_table=strided[:, ::2], output=torch.empty_like(qd), softmax_scale=SCALE,
+                             fallback=lambda: fell_back.append(1))
+    hooked = torch.full_like(qd, float("nan"))
+    calls = []
+    router.prefill_attention(layer_name=layer, plan=plan, query=qd, key_cache=kd, value_cache=vd, block_table=btd,
+                             output=hooked, softmax_scale=SCALE, before_direct=lambda: calls.append(1))
+    torch.cuda.synchronize()
+    assert fell_back == [1] and calls == [1] and torch.equal(hooked, want)
+    counters = stats.snapshot()["counters"]
+    assert counters["layer_direct"] == 2 and counters["layer_fia_reason:block_table_unsupported"] == 1
+    assert counters.get("runtime_error", 0) == 0
