@@ -44,6 +44,10 @@ HIP_FLAGS = [
     # Keep MFMA accumulators in VGPRs: the softmax rescales them every tile,
     # and VALU cannot operate on AGPRs without copies.
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # Preload the attention kernel's leading scalar arguments (the fields its
+    # prologue needs first) into SGPRs at wave launch; 16 dwords is the most
+    # the user SGPRs hold, and only scalar arguments qualify.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     # Device code only: no NaN operands, so fmaxf needs no quieting
     # canonicalisation of its inputs (which doubled the row-max work).  The
     # kernels never form NaN themselves (masked scores are -inf and an
