@@ -41,9 +41,10 @@ extern "C" {
 /* A non-empty workspace starts with this many bytes of arrival words, one
  * per split row block, KV head and workgroup position; the split-KV partials
  * follow.  A workspace's contents before a call do not matter (as the
- * reference's workspace, it is scratch): each word carries a tag unique to
- * the launch that wrote it, and a word with another launch's tag counts as
- * zero.  One workspace serves any sequence of calls on one stream. */
+ * reference's workspace, it is scratch): each word carries the arrival tag
+ * the library keeps for that workspace address, and a word with any other
+ * tag counts as zero.  One workspace serves any sequence of calls on one
+ * stream; calls that overlap in time on one workspace race. */
 #define TM_WORKSPACE_COUNTER_BYTES 65536
 
 /* No call needs more workspace than this (64 MiB): the planner keeps every

@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <vector>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/trianglemix.h"
 #include "trianglemix_kernel.h"
@@ -388,9 +389,9 @@ int plan_call(bool sparse, int64_t query_tokens, int64_t query_start, int64_t se
   return TM_OK;
 }
 
-// Arrival tag of one launch with split row blocks: nonzero and below 2^48,
-// different for every launch of the process (and, by its seed, unlikely to
-// meet another process's tags in a shared workspace).
+// A fresh arrival tag: nonzero and below 2^48, different from every other tag
+// this process hands out (and, by its seed, unlikely to meet another
+// process's tags in a shared workspace).
 unsigned long long next_epoch() {
   static std::atomic<unsigned long long> counter{[] {
     const unsigned long long t = (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count();
@@ -400,6 +401,31 @@ unsigned long long next_epoch() {
     const unsigned long long e = counter.fetch_add(1, std::memory_order_relaxed) & tmx::kEpochMask;
     if (e != 0) return e;
   }
+}
+
+// Arrival tag of a launch on `workspace`: one per workspace address, kept
+// across calls.  Every completed launch leaves its arrival words at (its
+// tag, count 0), so the next launch on the same workspace -- which gets the
+// same tag -- counts each arrival with one fetch-and-add; a word with any
+// other content (another address's tag, a fresh or reused buffer, garbage)
+// is foreign and takes the install.  Only completed launches write a word
+// with this tag, and launches that overlap on one workspace race anyway, so
+// a word carrying it always has count 0 when a launch starts.  A small
+// direct-mapped table holds the tags; an evicted address gets a fresh tag
+// on its next call (one install per word, then fast again).
+unsigned long long workspace_epoch(const void* workspace) {
+  constexpr int kSlots = 64;
+  struct Slot {
+    const void* workspace;
+    unsigned long long epoch;
+  };
+  static Slot slots[kSlots] = {};
+  static std::mutex mutex;
+  const uintptr_t a = (uintptr_t)workspace;
+  Slot& s = slots[(a >> 8 ^ a >> 16 ^ a >> 24) % kSlots];
+  std::lock_guard<std::mutex> lock(mutex);
+  if (s.workspace != workspace || s.epoch == 0) s = Slot{workspace, next_epoch()};
+  return s.epoch;
 }
 
 int launch(bool sparse, const void* query, const void* key_cache, const void* value_cache,
@@ -465,7 +491,7 @@ int launch(bool sparse, const void* query, const void* key_cache, const void* va
   const bool split = g.split_row_blocks > 0;
   p.counters = split ? static_cast<unsigned long long*>(workspace) : nullptr;
   p.partials = split ? reinterpret_cast<float*>(static_cast<char*>(workspace) + tmx::kCounterBytes) : nullptr;
-  p.epoch = split ? next_epoch() : 0;
+  p.epoch = split ? workspace_epoch(workspace) : 0;
   p.num_pages = (int)num_pages;
   p.query_start = (int)query_start;
   p.seq_len = (int)seq_len;

@@ -35,10 +35,11 @@ constexpr int64_t kPartialBytes = kPartialFloats * 4;
 // partials of the split row blocks' items.  A word holds the launch's 48-bit
 // epoch above a 16-bit arrival count; a word carrying another epoch counts as
 // zero, so the workspace may hold anything before a launch (the reference's
-// workspace is plain scratch).  The workgroup that completes a row block
-// clears its word, so a graph that replays one launch (one epoch) finds it
-// clear again.  The counter block has a fixed size, so the partials start at
-// the same offset for every geometry.
+// workspace is plain scratch).  The host keeps one epoch per workspace
+// address, and the workgroup that completes a row block leaves its word at
+// (epoch, 0): the next launch on that workspace, or the next replay of a
+// captured one, finds its words clean.  The counter block has a fixed size,
+// so the partials start at the same offset for every geometry.
 constexpr int64_t kCounterBytes = 65536;
 constexpr int kMaxSplitRowBlocks = int(kCounterBytes / 8 / (kKvHeads * 2));  // 512
 constexpr int kEpochShift = 16;

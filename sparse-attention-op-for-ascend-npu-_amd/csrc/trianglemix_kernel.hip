@@ -1068,9 +1068,12 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   __syncthreads();
   TM_PHASE(17);
   if (!s_last) return;
-  // Every split has arrived: clear the word, so that a replay of this very
-  // launch (same epoch, e.g. from a HIP graph) counts from zero again.
-  if (tid == 0) __hip_atomic_store(ctr, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Every split has arrived: leave the word at this launch's epoch with a
+  // count of zero.  The next launch on this workspace carries the same epoch
+  // (the host keeps one per workspace, and a HIP graph replays its captured
+  // one), so each of its arrivals is counted by its fetch-and-add alone,
+  // without the install a foreign word takes.
+  if (tid == 0) __hip_atomic_store(ctr, p.epoch << kEpochShift, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // One pass over the splits, kMergeBatch at a time with all of a batch's
   // loads in flight: a batch that raises the running max rescales what is

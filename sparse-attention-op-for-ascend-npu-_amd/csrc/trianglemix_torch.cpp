@@ -29,7 +29,7 @@
 // workspace (at most TM_MAX_WORKSPACE_BYTES), it comes from PyTorch's caching
 // allocator, as the reference's EXEC_NPU_CMD takes the aclnn workspace from
 // torch_npu's.  Its contents do not matter (the library tags each arrival
-// word with its launch), so no buffer is ever cleared.  Outside stream
+// word for its workspace), so no buffer is ever cleared.  Outside stream
 // capture one buffer is kept per (device, stream) and shared by the launches
 // on that stream, which run in order; a call that needs more replaces it,
 // and the old buffer goes back to the caching allocator, which hands its

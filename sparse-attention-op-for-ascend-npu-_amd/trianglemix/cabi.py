@@ -64,7 +64,7 @@ def chunk_plan(query_tokens: int, query_start: int, seq_len: int, prompt_len: in
 
 # Split-KV workspace per (device, stream), at most MAX_WORKSPACE_BYTES.  Its
 # contents before a call do not matter (the library tags every arrival word
-# with its launch), so a buffer is never cleared.  One buffer is kept per
+# for its workspace), so a buffer is never cleared.  One buffer is kept per
 # (device, stream), allocated on that stream; a call that needs more replaces
 # it, and PyTorch's caching allocator hands the old buffer's memory out again
 # only in that stream's order, after the work queued on it.

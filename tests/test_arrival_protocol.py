@@ -4,13 +4,15 @@
 workgroup position): the launch's 48-bit epoch above a 16-bit count.  An arrival adds one (fetch-and-add);
 if the word it added to carried another epoch, it installs its own epoch with a count of one, or counts
 itself under an epoch another arrival installed, by compare-and-swap from the value last seen.  The arrival
-whose count reaches the split count merges.  Workspace contents are arbitrary before a launch, so the
-initial word may be anything.
+whose count reaches the split count merges, then leaves the word at (epoch, 0): the host keeps one epoch per
+workspace address, so the next launch on that workspace (or the next replay of a captured one) finds its
+words clean and counts each arrival with its fetch-and-add alone.  Workspace contents are otherwise
+arbitrary before a launch, so the initial word may be anything.
 
 This file models each arrival as the sequence of atomic steps the kernel performs (the kernel's two atomic
 operations, each indivisible) and explores every interleaving of two and three arrivals from initial words
-that are clean, cleared by a previous launch, carry another epoch at every count, or sit one below a carry
-into the epoch field.  In every execution exactly one arrival must reach the split count, every arrival
+that are zero, left clean by a previous launch on the workspace (this epoch, count 0), carry another epoch
+at every count, or sit one below a carry into the epoch field.  In every execution exactly one arrival must reach the split count, every arrival
 must end in a bounded number of steps, and the word must end as (epoch, splits).  A planted variant that
 skips the install step (trusting any word) fails on a foreign word.
 """
@@ -46,6 +48,7 @@ def run_schedule(initial: int, epoch: int, n: int, order, trust_any_word=False):
     gens = [arrival(epoch, trust_any_word) for _ in range(n)]
     pending = [next(g) for g in gens]
     result = [None] * n
+    atomics = [0] * n
     steps = 0
     order = iter(order)
     while any(r is None for r in result):
@@ -56,6 +59,7 @@ def run_schedule(initial: int, epoch: int, n: int, order, trust_any_word=False):
         if result[i] is not None:
             i = live[0]
         op = pending[i]
+        atomics[i] += 1
         if op[0] == "add":
             reply = word
             word = (word + op[1]) & MASK64
@@ -69,11 +73,18 @@ def run_schedule(initial: int, epoch: int, n: int, order, trust_any_word=False):
             pending[i] = gens[i].send(reply)
         except StopIteration as stop:
             result[i] = stop.value
+    run_schedule.atomics = atomics
     return word, result
 
 
+def merge_and_reset(word: int, epoch: int) -> int:
+    """The last arrival's reset after its merge: the word is left at (epoch, 0)."""
+    assert word & ((1 << SHIFT) - 1) != 0
+    return epoch << SHIFT
+
+
 EPOCH = 0x1234_5678_9ABC
-INITIAL_WORDS = [0, (EPOCH - 1) << SHIFT, ((EPOCH + 7) << SHIFT) + 3, ((EPOCH - 1) << SHIFT) | 0xFFFF,
+INITIAL_WORDS = [0, EPOCH << SHIFT, (EPOCH - 1) << SHIFT, ((EPOCH + 7) << SHIFT) + 3, ((EPOCH - 1) << SHIFT) | 0xFFFF,
                  0xFFFF_FFFF_FFFF_FFFF, (0xDEAD_BEEF << SHIFT) + 1]
 
 
@@ -97,9 +108,28 @@ def test_cleared_word_takes_one_atomic_after_the_first_arrival():
     assert counts == [1, 2, 3] and word == (EPOCH << SHIFT) + 3
 
 
+def test_a_word_left_by_the_previous_launch_takes_one_atomic_per_arrival():
+    # launch 1 on a foreign word installs the epoch; its last arrival leaves (epoch, 0); launch 2 with the
+    # same epoch (the same workspace) counts every arrival by its fetch-and-add alone, in every order
+    word, counts = run_schedule(0xFFFF_FFFF_FFFF_FFFF, EPOCH, 3, [0, 1, 2, 0, 1, 2])
+    assert sorted(counts) == [1, 2, 3]
+    word = merge_and_reset(word, EPOCH)
+    for order in _schedules(3, 6):
+        final, counts = run_schedule(word, EPOCH, 3, order)
+        assert sorted(counts) == [1, 2, 3] and final == (EPOCH << SHIFT) + 3, order
+        assert run_schedule.atomics == [1, 1, 1], order
+
+
+def test_a_word_left_for_another_workspace_is_foreign():
+    # a word another workspace's launches left clean, (other epoch, 0), seen by this epoch: installed anew
+    word, counts = run_schedule((EPOCH + 1) << SHIFT, EPOCH, 2, [0, 1, 0, 1])
+    assert sorted(counts) == [1, 2] and word == (EPOCH << SHIFT) + 2
+    assert sum(run_schedule.atomics) > 2
+
+
 def test_trusting_any_word_fails_on_a_foreign_word():
     # the planted variant counts from whatever the word held: right only when its count field happens to be
     # zero, wrong for an interrupted launch's word (count 3) and for garbage
-    for initial in INITIAL_WORDS[1:]:
+    for initial in INITIAL_WORDS[2:]:
         _, counts = run_schedule(initial, EPOCH, 2, [0, 1], trust_any_word=True)
         assert (sorted(counts) == [1, 2]) == (initial & 0xFFFF == 0), hex(initial)
