@@ -429,7 +429,8 @@ def median_ms(run, reps: int, windows: int = 3) -> float:
 
 
 def long_context_points(seed: int, lengths) -> list[dict]:
-    """Whole prefills (chunk 2048), sparse vs dense, one HIP graph of the chunk launches per L; ABBA windows."""
+    """Whole prefills (chunk 2048), sparse vs dense, one HIP graph of the chunk launches per L; the sparse
+    graph's timing windows, then the dense graph's."""
     import torch
 
     from trianglemix.workload import SCALE, chunk_flops, prompt_chunks
@@ -460,11 +461,16 @@ def long_context_points(seed: int, lengths) -> list[dict]:
                 dense_op(q[c.query_start:c.seq_len], kc, vc, table, c.query_start, c.seq_len, SCALE,
                          out=out[c.query_start:c.seq_len])
 
-        gs, gd = graph_of(sparse_step), graph_of(dense_step)
-        gs.replay()
-        gd.replay()
+        # The sparse prefill is timed first, in windows of its own, and the dense one after it: at these
+        # lengths a dense window runs 10-150 ms at full power, and a short sparse window right after one
+        # (as ABBA order would put it) runs at a lowered clock.
         reps = 4 if L >= 131072 else (10 if L >= 32768 else 40)
-        tot_s, win_s, tot_d, win_d = abba(gs.replay, gd.replay, reps, 4)
+        gs = graph_of(sparse_step)
+        gs.replay()
+        tot_s, win_s, _, _ = abba(gs.replay, None, reps, 4)
+        gd = graph_of(dense_step)
+        gd.replay()
+        tot_d, win_d, _, _ = abba(gd.replay, None, reps, 4)
         ms_s, ms_d = tot_s / reps, tot_d / reps
         fs = sum(chunk_flops(c) for c in chunks)
         fd = sum(chunk_flops(c, dense=True) for c in chunks)
@@ -498,7 +504,8 @@ def config4_curve(args) -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 Q/K/V from the GPU generator, random page table)",
         "config": {"workload": "config4: one request per L, chunked prefill of 2048, Hq=32 Hkv=8 D=128 page=128, "
-                               "one layer; each prefill is one HIP graph of its chunk launches"},
+                               "one layer; each prefill is one HIP graph of its chunk launches, timed in windows of "
+                               "its own (sparse first, then dense)"},
         "curve": curve,
         "crossover_L": min(wins) if wins else None,
         "crossover_note": "smallest measured L whose whole sparse prefill beats the dense one; L=1024 is one "
