@@ -18,7 +18,11 @@ workspace exceeds 64 MiB.  Checks, all through the C ABI:
   every row against the oracle;
 * a split chunk on a workspace holding garbage (all 0xFF, random bytes, the
   words an interrupted launch would leave) is bit-identical to one on a fresh
-  workspace, and so is a repeat on the same workspace.
+  workspace, and so is a repeat on the same workspace;
+* one workspace carried through a sequence of split chunks of different
+  shapes (the library keeps one arrival tag per workspace, and each chunk's
+  arrival words sit at positions another chunk's used) gives every chunk the
+  bits of a fresh workspace.
 
 Tolerances as everywhere: max-abs 2e-2, mean-abs 2e-3, rel-L2 2e-2.
 """
@@ -191,6 +195,44 @@ def test_workspace_contents_do_not_matter(gpu, dense):
         for repeat in range(2):  # the second call finds the words the first left
             got = _run(gpu, qd, kd, vd, btd, qs, seq, prompt, ws)
             assert torch.equal(got, reference), (name, repeat)
+
+
+# (query_start, query_tokens, seq_len, prompt_len or None for the dense companion): split chunks of both
+# workgroup shapes, two to eight splits per row, dense-tail and dense rows
+SHARED_WORKSPACE_CHUNKS = [
+    (7680, 512, 8192, 8192),     # KV quarters, three splits per dense-tail row
+    (7680, 512, 8192, None),     # dense companion, every row split
+    (8192, 128, 8320, 8320),     # KV quarters, four splits per row
+    (6144, 2048, 8192, 8192),    # KV halves, split dense-tail rows among unsplit sparse ones
+    (16256, 128, 16384, 16384),  # long dense-tail rows
+    (7680, 512, 8192, 8192),     # the first chunk again, on words the others left
+]
+
+
+def test_one_workspace_across_split_chunks_of_different_shapes(gpu):
+    """One workspace through a sequence of split chunks whose arrival words overlap one another's (the
+    layout depends on the split row blocks and the workgroup shape): every chunk equals its run on a fresh
+    workspace, bit for bit.  The library keeps one arrival tag per workspace and each completed launch
+    leaves its words at (tag, 0), so a later chunk meets clean words of its own tag, words another shape
+    left and never-touched words at once."""
+    need = max(cabi.workspace_size(tq, qs, seq, prompt) for qs, tq, seq, prompt in SHARED_WORKSPACE_CHUNKS)
+    assert 0 < need <= cabi.MAX_WORKSPACE_BYTES
+    shared = torch.full((need,), 0xFF, dtype=torch.uint8, device=gpu)
+    caches = {}
+    for i, (qs, tq, seq, prompt) in enumerate(SHARED_WORKSPACE_CHUNKS):
+        print(f"shared workspace: chunk {i} qs={qs} tq={tq} seq={seq} prompt={prompt}", flush=True)
+        assert cabi.workspace_size(tq, qs, seq, prompt) > cabi.WORKSPACE_COUNTER_BYTES, "the chunk must split"
+        if seq not in caches:
+            k, v, bt = make_cache(seq, 80 + seq % 97, std=1.0)
+            caches[seq] = (k.to(gpu), v.to(gpu), bt.to(gpu))
+        kd, vd, btd = caches[seq]
+        qd = make_query(tq, 90 + i % 5, std=1.0).to(gpu)
+        fresh = torch.zeros(cabi.workspace_size(tq, qs, seq, prompt), dtype=torch.uint8, device=gpu)
+        expected = _run(gpu, qd, kd, vd, btd, qs, seq, prompt, fresh)
+        assert torch.isfinite(expected.float()).all(), i
+        for repeat in range(2):
+            got = _run(gpu, qd, kd, vd, btd, qs, seq, prompt, shared)
+            assert torch.equal(got, expected), (i, repeat)
 
 
 def test_captured_split_chunk_replays_bit_identical(gpu):
