@@ -86,7 +86,8 @@ class _Execution:
         self.launches += ev.launches
         self.saved_qk += ev.saved_qk
         self.enqueue_ns += ev.enqueue_ns
-        self.enqueue_max = max(self.enqueue_max, ev.enqueue_ns)
+        if ev.enqueue_ns > self.enqueue_max:  # (not max(): this runs for every direct layer call)
+            self.enqueue_max = ev.enqueue_ns
 
     def as_dict(self) -> dict[str, Any]:
         seen = self.direct + self.dense
