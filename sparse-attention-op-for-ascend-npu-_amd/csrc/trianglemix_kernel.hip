@@ -1044,10 +1044,11 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   __syncthreads();
   // Arrival word of (KV head, row block, workgroup position): this launch's
   // epoch above the count of splits arrived under it.  A word that carries
-  // another epoch (left by another launch, cleared, or whatever the
-  // workspace held) counts as zero.  Each arrival adds one: when the word
-  // already carries this launch's epoch that is its count (one round trip,
-  // the case of every arrival after the first).  An arrival that finds
+  // another epoch (another workspace's launches, a fresh buffer, or whatever
+  // the workspace held) counts as zero.  Each arrival adds one: when the word
+  // already carries this launch's epoch that is its count (one round trip:
+  // every arrival on a word a previous launch of this workspace left clean,
+  // and every arrival after the first otherwise).  An arrival that finds
   // another epoch has added to a void word; it then installs this launch's
   // epoch with a count of one, or -- if another arrival installed it first
   // -- adds itself under it, by compare-and-swap from the value last seen.
