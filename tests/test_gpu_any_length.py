@@ -22,7 +22,8 @@ workspace exceeds 64 MiB.  Checks, all through the C ABI:
 * one workspace carried through a sequence of split chunks of different
   shapes (the library keeps one arrival tag per workspace, and each chunk's
   arrival words sit at positions another chunk's used) gives every chunk the
-  bits of a fresh workspace.
+  bits of a fresh workspace, and so do 80 workspaces used in turn (more than
+  the library's table of tags holds).
 
 Tolerances as everywhere: max-abs 2e-2, mean-abs 2e-3, rel-L2 2e-2.
 """
@@ -233,6 +234,24 @@ def test_one_workspace_across_split_chunks_of_different_shapes(gpu):
         for repeat in range(2):
             got = _run(gpu, qd, kd, vd, btd, qs, seq, prompt, shared)
             assert torch.equal(got, expected), (i, repeat)
+
+
+def test_more_workspaces_than_the_tag_table_holds(gpu):
+    """The library keeps one arrival tag per workspace address in a table of 64 slots; 80 workspaces used
+    in turn, twice over, evict one another's entries (an evicted address gets a fresh tag, so its words
+    from the first pass are foreign in the second).  Every call equals the run on a fresh workspace."""
+    qs, tq, seq = 7680, 512, 8192
+    need = cabi.workspace_size(tq, qs, seq, seq)
+    assert need > cabi.WORKSPACE_COUNTER_BYTES
+    k, v, bt = make_cache(seq, 95, std=1.0)
+    qd, kd, vd, btd = make_query(tq, 96, std=1.0).to(gpu), k.to(gpu), v.to(gpu), bt.to(gpu)
+    expected = _run(gpu, qd, kd, vd, btd, qs, seq, seq, torch.zeros(need, dtype=torch.uint8, device=gpu))
+    workspaces = [torch.empty(need, dtype=torch.uint8, device=gpu) for _ in range(80)]
+    for sweep in range(2):
+        print(f"tag table: pass {sweep} over {len(workspaces)} workspaces", flush=True)
+        for i, ws in enumerate(workspaces):
+            got = _run(gpu, qd, kd, vd, btd, qs, seq, seq, ws)
+            assert torch.equal(got, expected), (sweep, i)
 
 
 def test_captured_split_chunk_replays_bit_identical(gpu):
