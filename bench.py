@@ -464,14 +464,18 @@ def long_context_points(seed: int, lengths) -> list[dict]:
         # The sparse prefill is timed first, in windows of its own, and the dense one after it: at these
         # lengths a dense window runs 10-150 ms at full power, and a short sparse window right after one
         # (as ABBA order would put it) runs at a lowered clock.
+        # The sparse prefill also gets a warm-up of a third of its timed replays (its windows follow the
+        # previous leg's dense work) and more replays than the dense one: they cost little.
         reps = 4 if L >= 131072 else (10 if L >= 32768 else 40)
+        reps_s = 3 * reps
         gs = graph_of(sparse_step)
-        gs.replay()
-        tot_s, win_s, _, _ = abba(gs.replay, None, reps, 4)
+        for _ in range(reps):
+            gs.replay()
+        tot_s, win_s, _, _ = abba(gs.replay, None, reps_s, 4)
         gd = graph_of(dense_step)
         gd.replay()
         tot_d, win_d, _, _ = abba(gd.replay, None, reps, 4)
-        ms_s, ms_d = tot_s / reps, tot_d / reps
+        ms_s, ms_d = tot_s / reps_s, tot_d / reps
         fs = sum(chunk_flops(c) for c in chunks)
         fd = sum(chunk_flops(c, dense=True) for c in chunks)
         curve.append({"L": L, "chunks": len(chunks), "sparse_ms": round(ms_s, 4), "dense_ms": round(ms_d, 4),
