@@ -20,6 +20,12 @@ Reported JSON line (rank 0 only):
   for this workload exists under profiles/, else null;
 * ``dense`` -- the same 16 chunks through the dense paged causal companion
   kernel, and the attention-time cut of sparse vs dense;
+* ``library_dense`` -- the same 16 chunks through PyTorch's own dense
+  attention (``scaled_dot_product_attention``, flash backend: AOTriton's
+  kernels on ROCm), causal lower-right, GQA in the kernel, on K/V gathered
+  into contiguous (1, Hkv, S, D) tensors outside the timed region (the
+  library gets no page table to follow), one HIP graph per step: a dense
+  baseline that is not this repository's own kernel;
 * ``kv_write`` -- the paged KV write upstream of the attention
   (``trianglemix::reshape_and_cache``): one chunk's fresh K/V into its pages,
   and the whole prompt in one call, with HBM GB/s against 8 TB/s;
@@ -204,6 +210,9 @@ def chunk_set_line(args, headline: bool) -> dict:
 
     traffic = read_traffic_summary() if headline else None
     kv_write = kv_write_bench(args, chunks, k, v, bt, dev) if args.only is None and headline else None
+    library = None
+    if args.only is None and (headline or args.workload == "config3"):
+        library = library_dense(chunks, qfull, k, v, bt, kd, vd, btd, args.steps, ms_sparse, ms_dense)
     errors = None
     if args.workload == "config3" and args.only is None:
         errors = oracle_errors(chunks, qfull, k, v, bt, m["outputs"])
@@ -260,6 +269,7 @@ def chunk_set_line(args, headline: bool) -> dict:
             "attention_time_cut": round(1.0 - ms_sparse / ms_dense, 4) if ms_dense == ms_dense else None,
             "timing": m["dense_stats"],
         },
+        "library_dense": library,
         "errors_vs_fp32": errors,
         "kv_write": kv_write,
         "cpu_baseline": cpu,
@@ -393,6 +403,96 @@ def headline_legs(args) -> dict:
     legs["config4"] = long_context_points(args.seed, (32768, 131072))
     legs["config5"] = layer_stack_summary(args.seed)
     return legs
+
+
+def library_dense(chunks, qfull, k, v, bt, kd, vd, btd, steps, ms_sparse, ms_dense) -> dict:
+    """The same chunks through PyTorch's own dense attention: ``scaled_dot_product_attention`` restricted to
+    its flash backend (AOTriton's kernels on ROCm; the memory-efficient backend if flash is refused), mask
+    ``causal_lower_right`` (row i of a chunk sees keys <= query_start + i, as the dense companion does),
+    GQA handled by the kernel.  K/V are gathered from the pages into contiguous (1, Hkv, S, D) tensors and
+    Q into (1, Hq, T, D) before timing.  One HIP graph of the chunk calls per step, each replay checked
+    against the eager result with eager work between replays; eager calls if capture is refused."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from torch.nn.attention.bias import causal_lower_right
+
+    from trianglemix.workload import SCALE, chunk_flops
+
+    dev = kd.device
+    order = bt[0].long()
+    kc, vc = k[order].flatten(0, 1), v[order].flatten(0, 1)  # (pages * page, Hkv, D) in logical order
+    qs = [qfull[c.query_start:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    ks = [kc[:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    vs = [vc[:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    masks = [causal_lower_right(c.seq_len - c.query_start, c.seq_len) for c in chunks]
+    outs = [None] * len(chunks)
+
+    def calls(backend):
+        with sdpa_kernel([backend]):
+            for i in range(len(chunks)):
+                outs[i] = F.scaled_dot_product_attention(qs[i], ks[i], vs[i], attn_mask=masks[i], scale=SCALE,
+                                                         enable_gqa=True)
+
+    backend, refused = None, {}
+    for b in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            calls(b)
+            torch.cuda.synchronize()
+            backend = b
+            break
+        except RuntimeError as e:
+            refused[b.name] = str(e).splitlines()[0][:200]
+    if backend is None:
+        return {"error": "no fused SDPA backend accepted the chunks", "refused": refused}
+    eager = [o.clone() for o in outs]
+
+    dense_op = torch.ops.trianglemix.dense_paged_causal_attention.out
+    ours = [torch.empty(c.seq_len - c.query_start, qfull.shape[1], qfull.shape[2], dtype=qfull.dtype, device=dev)
+            for c in chunks]
+
+    def dense_calls():
+        for c, q, o in zip(chunks, qs, ours):
+            dense_op(q[0].permute(1, 0, 2).contiguous(), kd, vd, btd, c.query_start, c.seq_len, SCALE, out=o)
+
+    dense_calls()
+    torch.cuda.synchronize()
+    max_abs = max((e[0].permute(1, 0, 2).float() - o.float()).abs().max().item() for e, o in zip(eager, ours))
+
+    run, graphed = (lambda: calls(backend)), True
+    try:
+        g = graph_of(run)
+        for _ in range(3):
+            for o in outs:
+                o.zero_()
+            dense_calls()  # eager work between replays
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            if not all(torch.equal(o, e) for o, e in zip(outs, eager)):
+                raise RuntimeError("graph replay differs from eager calls")
+        run = g.replay
+    except RuntimeError:
+        graphed = False
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    tot, win, _, _ = abba(run, None, steps, max(2, min(10, steps // 5 * 2)))
+    ms = tot / steps
+    dense_flops = sum(chunk_flops(c, dense=True) for c in chunks)
+    return {
+        "impl": (f"torch.nn.functional.scaled_dot_product_attention, {backend.name} backend (AOTriton on ROCm), "
+                 "causal_lower_right, enable_gqa; K/V contiguous (gathered from the pages before timing)"),
+        "graph": graphed,
+        "refused_backends": refused or None,
+        "ms_per_step": round(ms, 5),
+        "us_per_chunk": round(ms * 1000.0 / len(chunks), 3),
+        "alg_tflops": round(dense_flops / (ms * 1e-3) / 1e12, 2),
+        "dense_companion_speedup": round(ms / ms_dense, 3) if ms_dense == ms_dense else None,
+        "sparse_speedup": round(ms / ms_sparse, 3) if ms_sparse == ms_sparse else None,
+        "max_abs_vs_dense_companion": max_abs,
+        "timing": timing_stats(win),
+    }
 
 
 def graph_of(step):
