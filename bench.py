@@ -47,7 +47,7 @@ Reported JSON line (rank 0 only):
 Detailed single-workload runs (one JSON line each, not the headline):
 ``--workload config1 | config3`` (same legs as the headline, that chunk set),
 ``--workload config4`` (the whole long-context curve, L = 1024 .. 131072, and
-the crossover), ``--workload config5`` (the layer stack with both gate sets,
+the crossover; each L also through PyTorch's own dense attention), ``--workload config5`` (the layer stack with both gate sets,
 the structured counter log and the vLLM-ROCm seam).
 """
 
@@ -405,26 +405,22 @@ def headline_legs(args) -> dict:
     return legs
 
 
-def library_dense(chunks, qfull, k, v, bt, kd, vd, btd, steps, ms_sparse, ms_dense) -> dict:
-    """The same chunks through PyTorch's own dense attention: ``scaled_dot_product_attention`` restricted to
+def sdpa_chunks(chunks, qs, ks, vs, between):
+    """PyTorch's own dense attention over a chunk sequence: ``scaled_dot_product_attention`` restricted to
     its flash backend (AOTriton's kernels on ROCm; the memory-efficient backend if flash is refused), mask
     ``causal_lower_right`` (row i of a chunk sees keys <= query_start + i, as the dense companion does),
-    GQA handled by the kernel.  K/V are gathered from the pages into contiguous (1, Hkv, S, D) tensors and
-    Q into (1, Hq, T, D) before timing.  One HIP graph of the chunk calls per step, each replay checked
-    against the eager result with eager work between replays; eager calls if capture is refused."""
+    GQA handled by the kernel.  ``qs[i]`` is chunk i's (1, Hq, T, D) query and ``ks[i]`` / ``vs[i]`` its
+    (1, Hkv, S, D) keys and values, all contiguous.  Returns (run, eager outputs, facts): ``run`` replays
+    one HIP graph of all the calls (three replays are first checked against the eager outputs, each after
+    ``between()`` has run eagerly) or, if capture is refused, makes the calls eagerly; ``run`` is None when
+    no fused backend accepts the chunks."""
     import torch
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
     from torch.nn.attention.bias import causal_lower_right
 
-    from trianglemix.workload import SCALE, chunk_flops
+    from trianglemix.workload import SCALE
 
-    dev = kd.device
-    order = bt[0].long()
-    kc, vc = k[order].flatten(0, 1), v[order].flatten(0, 1)  # (pages * page, Hkv, D) in logical order
-    qs = [qfull[c.query_start:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
-    ks = [kc[:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
-    vs = [vc[:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
     masks = [causal_lower_right(c.seq_len - c.query_start, c.seq_len) for c in chunks]
     outs = [None] * len(chunks)
 
@@ -443,29 +439,21 @@ def library_dense(chunks, qfull, k, v, bt, kd, vd, btd, steps, ms_sparse, ms_den
             break
         except RuntimeError as e:
             refused[b.name] = str(e).splitlines()[0][:200]
+    facts = {"impl": None if backend is None else
+             (f"torch.nn.functional.scaled_dot_product_attention, {backend.name} backend (AOTriton on ROCm), "
+              "causal_lower_right, enable_gqa; Q/K/V contiguous (gathered from the pages before timing)"),
+             "refused_backends": refused or None}
     if backend is None:
-        return {"error": "no fused SDPA backend accepted the chunks", "refused": refused}
+        facts["error"] = "no fused SDPA backend accepted the chunks"
+        return None, None, facts
     eager = [o.clone() for o in outs]
-
-    dense_op = torch.ops.trianglemix.dense_paged_causal_attention.out
-    ours = [torch.empty(c.seq_len - c.query_start, qfull.shape[1], qfull.shape[2], dtype=qfull.dtype, device=dev)
-            for c in chunks]
-
-    def dense_calls():
-        for c, q, o in zip(chunks, qs, ours):
-            dense_op(q[0].permute(1, 0, 2).contiguous(), kd, vd, btd, c.query_start, c.seq_len, SCALE, out=o)
-
-    dense_calls()
-    torch.cuda.synchronize()
-    max_abs = max((e[0].permute(1, 0, 2).float() - o.float()).abs().max().item() for e, o in zip(eager, ours))
-
     run, graphed = (lambda: calls(backend)), True
     try:
         g = graph_of(run)
         for _ in range(3):
             for o in outs:
                 o.zero_()
-            dense_calls()  # eager work between replays
+            between()
             torch.cuda.synchronize()
             g.replay()
             torch.cuda.synchronize()
@@ -474,6 +462,38 @@ def library_dense(chunks, qfull, k, v, bt, kd, vd, btd, steps, ms_sparse, ms_den
         run = g.replay
     except RuntimeError:
         graphed = False
+    facts["graph"] = graphed
+    return run, eager, facts
+
+
+def library_dense(chunks, qfull, k, v, bt, kd, vd, btd, steps, ms_sparse, ms_dense) -> dict:
+    """The same chunks through PyTorch's own dense attention (``sdpa_chunks``), on Q/K/V gathered into
+    contiguous tensors before timing, timed in windows of its own; its largest output difference from the
+    dense companion."""
+    import torch
+
+    from trianglemix.workload import SCALE, chunk_flops
+
+    dev = kd.device
+    order = bt[0].long()
+    kc, vc = k[order].flatten(0, 1), v[order].flatten(0, 1)  # (pages * page, Hkv, D) in logical order
+    qs = [qfull[c.query_start:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    ks = [kc[:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    vs = [vc[:c.seq_len].to(dev).permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    dense_op = torch.ops.trianglemix.dense_paged_causal_attention.out
+    ours = [torch.empty(c.seq_len - c.query_start, qfull.shape[1], qfull.shape[2], dtype=qfull.dtype, device=dev)
+            for c in chunks]
+
+    def dense_calls():
+        for c, q, o in zip(chunks, qs, ours):
+            dense_op(q[0].permute(1, 0, 2).contiguous(), kd, vd, btd, c.query_start, c.seq_len, SCALE, out=o)
+
+    run, eager, facts = sdpa_chunks(chunks, qs, ks, vs, dense_calls)
+    if run is None:
+        return facts
+    dense_calls()
+    torch.cuda.synchronize()
+    max_abs = max((e[0].permute(1, 0, 2).float() - o.float()).abs().max().item() for e, o in zip(eager, ours))
     for _ in range(3):
         run()
     torch.cuda.synchronize()
@@ -481,10 +501,7 @@ def library_dense(chunks, qfull, k, v, bt, kd, vd, btd, steps, ms_sparse, ms_den
     ms = tot / steps
     dense_flops = sum(chunk_flops(c, dense=True) for c in chunks)
     return {
-        "impl": (f"torch.nn.functional.scaled_dot_product_attention, {backend.name} backend (AOTriton on ROCm), "
-                 "causal_lower_right, enable_gqa; K/V contiguous (gathered from the pages before timing)"),
-        "graph": graphed,
-        "refused_backends": refused or None,
+        **facts,
         "ms_per_step": round(ms, 5),
         "us_per_chunk": round(ms * 1000.0 / len(chunks), 3),
         "alg_tflops": round(dense_flops / (ms * 1e-3) / 1e12, 2),
@@ -528,9 +545,10 @@ def median_ms(run, reps: int, windows: int = 3) -> float:
     return statistics.median(times)
 
 
-def long_context_points(seed: int, lengths) -> list[dict]:
+def long_context_points(seed: int, lengths, library: bool = False) -> list[dict]:
     """Whole prefills (chunk 2048), sparse vs dense, one HIP graph of the chunk launches per L; the sparse
-    graph's timing windows, then the dense graph's."""
+    graph's timing windows, then the dense graph's; with ``library``, then PyTorch's own dense attention
+    over the same chunks (``sdpa_chunks``, on contiguous copies of each chunk's Q/K/V)."""
     import torch
 
     from trianglemix.workload import SCALE, chunk_flops, prompt_chunks
@@ -578,17 +596,46 @@ def long_context_points(seed: int, lengths) -> list[dict]:
         ms_s, ms_d = tot_s / reps_s, tot_d / reps
         fs = sum(chunk_flops(c) for c in chunks)
         fd = sum(chunk_flops(c, dense=True) for c in chunks)
-        curve.append({"L": L, "chunks": len(chunks), "sparse_ms": round(ms_s, 4), "dense_ms": round(ms_d, 4),
-                      "speedup": round(ms_d / ms_s, 3), "sparse_gflop": round(fs / 1e9, 2),
-                      "dense_gflop": round(fd / 1e9, 2), "sparse_tflops": round(fs / (ms_s * 1e-3) / 1e12, 1),
-                      "dense_tflops": round(fd / (ms_d * 1e-3) / 1e12, 1),
-                      "sparse_us_per_chunk": round(ms_s * 1000.0 / len(chunks), 2),
-                      "sparse_window_iqr_ms": timing_stats(win_s)["iqr_ms"]})
+        point = {"L": L, "chunks": len(chunks), "sparse_ms": round(ms_s, 4), "dense_ms": round(ms_d, 4),
+                 "speedup": round(ms_d / ms_s, 3), "sparse_gflop": round(fs / 1e9, 2),
+                 "dense_gflop": round(fd / 1e9, 2), "sparse_tflops": round(fs / (ms_s * 1e-3) / 1e12, 1),
+                 "dense_tflops": round(fd / (ms_d * 1e-3) / 1e12, 1),
+                 "sparse_us_per_chunk": round(ms_s * 1000.0 / len(chunks), 2),
+                 "sparse_window_iqr_ms": timing_stats(win_s)["iqr_ms"]}
+        if library:
+            point["library"] = library_prefill(chunks, q, kc, vc, table, out, gd.replay, reps, ms_d)
+        curve.append(point)
         print(f"# config4 L={L}: sparse {ms_s:.3f} ms dense {ms_d:.3f} ms x{ms_d / ms_s:.2f}", file=sys.stderr,
               flush=True)
         del kc, vc, q, out, gs, gd
         torch.cuda.empty_cache()
     return curve
+
+
+def library_prefill(chunks, q, kc, vc, table, dense_out, between, reps: int, ms_dense: float) -> dict:
+    """One whole prefill through PyTorch's own dense attention (``sdpa_chunks``): each chunk's Q/K/V copied
+    into contiguous tensors before timing, then ``reps`` timed replays; the largest difference of its
+    outputs from the dense companion's (``dense_out``, all rows of the prompt)."""
+    import torch
+
+    kl = kc[table[0].long()].flatten(0, 1)  # (pages * page, Hkv, D) in logical order
+    vl = vc[table[0].long()].flatten(0, 1)
+    qs = [q[c.query_start:c.seq_len].permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    ks = [kl[:c.seq_len].permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    vs = [vl[:c.seq_len].permute(1, 0, 2).contiguous().unsqueeze(0) for c in chunks]
+    del kl, vl
+    run, eager, facts = sdpa_chunks(chunks, qs, ks, vs, between)
+    if run is None:
+        return facts
+    max_abs = max((e[0].permute(1, 0, 2).float() - dense_out[c.query_start:c.seq_len].float()).abs().max().item()
+                  for c, e in zip(chunks, eager))
+    run()
+    torch.cuda.synchronize()
+    tot, _, _, _ = abba(run, None, reps, min(4, reps))
+    ms = tot / reps
+    del qs, ks, vs, eager
+    return {**facts, "ms": round(ms, 4), "vs_dense_companion": round(ms / ms_dense, 3),
+            "max_abs_vs_dense_companion": max_abs}
 
 
 def config4_curve(args) -> int:
@@ -597,7 +644,7 @@ def config4_curve(args) -> int:
 
     native.load_hip_library()
     native.load_triangle_mix_adapter()
-    curve = long_context_points(args.seed, (1024, 2048, 4096, 8192, 16384, 32768, 131072))
+    curve = long_context_points(args.seed, (1024, 2048, 4096, 8192, 16384, 32768, 131072), library=True)
     wins = [p["L"] for p in curve if p["sparse_ms"] < p["dense_ms"]]
     line = {
         "metric": "long-context prefill attention, sparse vs dense (config4, chunk 2048)",
@@ -609,7 +656,8 @@ def config4_curve(args) -> int:
         "data": "synthetic (seeded N(0,1) bf16 Q/K/V from the GPU generator, random page table)",
         "config": {"workload": "config4: one request per L, chunked prefill of 2048, Hq=32 Hkv=8 D=128 page=128, "
                                "one layer; each prefill is one HIP graph of its chunk launches, timed in windows of "
-                               "its own (sparse first, then dense)"},
+                               "its own (sparse first, then dense, then PyTorch's own dense attention on "
+                               "contiguous copies of each chunk's Q/K/V: `library`)"},
         "curve": curve,
         "crossover_L": min(wins) if wins else None,
         "crossover_note": "smallest measured L whose whole sparse prefill beats the dense one; L=1024 is one "
