@@ -23,7 +23,9 @@ workspace exceeds 64 MiB.  Checks, all through the C ABI:
   shapes (the library keeps one arrival tag per workspace, and each chunk's
   arrival words sit at positions another chunk's used) gives every chunk the
   bits of a fresh workspace, and so do 80 workspaces used in turn (more than
-  the library's table of tags holds).
+  the library's table of tags holds);
+* split chunks in flight on two streams at once through the torch ops (one
+  adapter workspace per stream) equal the same calls run alone.
 
 Tolerances as everywhere: max-abs 2e-2, mean-abs 2e-3, rel-L2 2e-2.
 """
@@ -287,6 +289,45 @@ def test_captured_split_chunk_replays_bit_identical(gpu):
         torch.cuda.synchronize()
         assert torch.equal(graph_out, eager), replay
         assert torch.equal(between, other_eager), replay
+
+
+def test_split_chunks_on_two_streams_at_once(gpu):
+    """Two streams running split chunks through the torch ops at the same time: the adapter keeps one
+    workspace per (device, stream), so calls in flight on different streams never share arrival words or
+    partials.  Four rounds, each enqueuing the TriangleMix op's last config-2 chunk on one stream and the
+    dense companion's on the other with no synchronisation between them; every output is bit-identical to
+    the same call run alone."""
+    qs, tq, seq = 7680, 512, 8192
+    assert cabi.workspace_size(tq, qs, seq, seq) > cabi.WORKSPACE_COUNTER_BYTES
+    assert cabi.workspace_size(tq, qs, seq, None) > cabi.WORKSPACE_COUNTER_BYTES
+    k, v, bt = make_cache(seq, 61, std=1.0)
+    kd, vd, btd = k.to(gpu), v.to(gpu), bt.to(gpu)
+    queries = [make_query(tq, 62 + i, std=1.0).to(gpu) for i in range(4)]
+    sparse_op = torch.ops.trianglemix.triangle_paged_sparse_attention.out
+    dense_op = torch.ops.trianglemix.dense_paged_causal_attention.out
+    alone_sparse, alone_dense = [], []
+    for qd in queries:
+        alone_sparse.append(torch.empty_like(qd))
+        sparse_op(qd, kd, vd, btd, qs, seq, seq, SCALE, out=alone_sparse[-1])
+        alone_dense.append(torch.empty_like(qd))
+        dense_op(qd, kd, vd, btd, qs, seq, SCALE, out=alone_dense[-1])
+    torch.cuda.synchronize()
+    got_sparse = [torch.full_like(qd, float("nan")) for qd in queries]
+    got_dense = [torch.full_like(qd, float("nan")) for qd in queries]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    print("two streams: 4 rounds of a split sparse and a split dense chunk", flush=True)
+    for i, qd in enumerate(queries):
+        first, second = (streams[0], streams[1]) if i % 2 == 0 else (streams[1], streams[0])
+        with torch.cuda.stream(first):
+            sparse_op(qd, kd, vd, btd, qs, seq, seq, SCALE, out=got_sparse[i])
+        with torch.cuda.stream(second):
+            dense_op(qd, kd, vd, btd, qs, seq, SCALE, out=got_dense[i])
+    torch.cuda.synchronize()
+    for i in range(len(queries)):
+        assert torch.equal(got_sparse[i], alone_sparse[i]), ("sparse", i)
+        assert torch.equal(got_dense[i], alone_dense[i]), ("dense", i)
 
 
 def test_router_routes_a_whole_long_prompt_direct(gpu):
