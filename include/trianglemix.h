@@ -153,7 +153,8 @@ int64_t tm_dense_paged_causal_attention_workspace_size(
 /*
  * The launch plan the entry points above use for one chunk geometry: the
  * workgroup shape (*kv_parts: 4 = two query heads over KV quarters, 2 = the
- * four heads of a GQA group over KV halves), the most tiles of 32 keys one
+ * four heads of a GQA group over KV halves, 1 = the four heads over the whole
+ * KV range, two workgroups per CU), the most tiles of 32 keys one
  * work item takes (*tiles_per_split) and the work items per KV head
  * (*items_per_kv_head).  dense != 0 plans the dense companion (prompt_len is
  * then ignored).  Returns TM_OK, or TM_ERR_INVALID_ARGUMENT for attributes the

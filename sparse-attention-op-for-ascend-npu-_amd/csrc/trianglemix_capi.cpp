@@ -83,9 +83,26 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
 //    128-512 (L = 4096-16384) the tile bound is the fastest rule or within
 //    1 % of it, against up to 9 % slower for halves on every split chunk and
 //    up to 12 % slower for quarters on every one.
+//
+// KV whole (four waves, one per head, every tile of the item; two workgroups
+// per CU) takes a TriangleMix chunk of at least kWholeMinRowBlocks row blocks
+// whose KV-halves plan splits no row block, when its simulated makespan
+// (below) is the shorter: a chunk of 64 sparse row blocks then fills the CUs
+// in one round where KV halves run two, and no KV-part merge remains; a chunk
+// holding long rows (a short prompt's dense tail) stays with KV halves, whose
+// waves take half of every such row.
+// Measured on MI355X (eager, one box): sparse middle chunks of 1536, 2048,
+// 3072 and 4096 rows 16 %, 12 %, 5 % and 12 % faster than KV halves, the
+// 2048-row chunks of an 8320- or 32768-token prompt 12-18 %; 1024-row chunks
+// (256 workgroups, one per CU) 15 % slower, a whole 2048-token prompt (its
+// 64-tile dense tail in one wave per row block) 17 % slower, chunks whose
+// dense tail splits 1-36 % slower (each split piece then runs all its tiles in
+// one wave), and so are most of the dense companion's chunks (their rows
+// split).
 constexpr int kHalvesMinRowBlocks = 17;
 constexpr int kHalvesSplitMinRowBlocks = 4;
 constexpr int64_t kHalvesDenseMinTiles = 2048;
+constexpr int kWholeMinRowBlocks = 48;
 
 // Split-KV sizing and shape choice.  A work item runs as 16 (KV quarters) or
 // 8 (KV halves) workgroups, one per CU, so each of the item's workgroup
@@ -136,8 +153,12 @@ struct PlanCosts {
 };
 constexpr PlanCosts kQuarterCosts{16, 4, 6, 1, 1};
 constexpr PlanCosts kHalfCosts{32, 2, 5, 3, 1};
-constexpr int kMaxSlots = 32;
-static_assert(kQuarterCosts.slots <= kMaxSlots && kHalfCosts.slots <= kMaxSlots, "simulated_makespan's slot heap");
+// KV whole: 8 workgroups per item, two per CU, one tile per iteration.  Only
+// plans without a split are costed for it (see choose_plan).
+constexpr PlanCosts kWholeCosts{64, 1, 5, 3, 1};
+constexpr int kMaxSlots = 64;
+static_assert(kQuarterCosts.slots <= kMaxSlots && kHalfCosts.slots <= kMaxSlots && kWholeCosts.slots <= kMaxSlots,
+              "simulated_makespan's slot heap");
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 constexpr int kFineSplitTiles = 768 / tmx::kKvTile;
 // Beyond this many items per candidate the simulation is skipped (its host
@@ -277,7 +298,16 @@ struct ChunkPlan {
 
 ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
   const int num_row_blocks = (int)row_tiles.size();
-  if (num_row_blocks >= kHalvesMinRowBlocks) return {2, choose_tiles_per_split(row_tiles, kHalfCosts).tiles_per_split};
+  if (num_row_blocks >= kHalvesMinRowBlocks) {
+    const SplitChoice halves = choose_tiles_per_split(row_tiles, kHalfCosts);
+    const int t = halves.tiles_per_split;
+    if (sparse && num_row_blocks >= kWholeMinRowBlocks && halves.makespan >= 0 &&
+        split_layout(row_tiles, t).split_row_blocks == 0 &&
+        simulated_makespan(row_tiles, t, kWholeCosts) < halves.makespan) {
+      return {1, t};
+    }
+    return {2, t};
+  }
   if (sparse) {
     // TriangleMix: the shape whose best plan has the shorter makespan.
     // Quarters take items of at most kLadderTop tiles here: with longer

@@ -129,8 +129,9 @@ struct KernelParams {
 // Enqueues the attention kernel (TriangleMix mask when `sparse`, plain causal
 // otherwise): one launch, split row blocks included.  kv_parts picks the
 // workgroup shape: 4 (two query heads x KV quarters, items_per_head x 16
-// workgroups) or 2 (the four heads of the GQA group x KV halves,
-// items_per_head x 8).
+// workgroups of eight waves), 2 (the four heads of the GQA group x KV halves,
+// items_per_head x 8 of eight waves) or 1 (the four heads x the whole KV
+// range, items_per_head x 8 of four waves, two per CU).
 hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, int kv_parts, hipStream_t stream);
 
 // Device address of this GPU's no-allocation scratch (kNoAllocScratchBytes,

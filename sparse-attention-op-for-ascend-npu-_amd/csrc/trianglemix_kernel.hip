@@ -3,19 +3,24 @@
 // Work decomposition
 // ------------------
 // A work item is (row block of 32 query tokens, KV head, KV split).  A
-// workgroup has eight wave64s, two per SIMD: (query head hl) x (KV part kq),
-// in one of two shapes (template parameter P, chosen per chunk by the host):
-//  * P = 4, KV quarters: each item runs as two workgroups, one per pair of the
-//    KV head's four GQA query heads; wave w owns the 32 rows {32 tokens} x
-//    {head 4*kvh + 2*hp + hl} and processes every fourth 32-key tile of the
-//    item (tiles kq, kq+4, ...).  A 512-token chunk fills the 256 CUs.
-//  * P = 2, KV halves: one workgroup holds all four heads of the group and
-//    every wave every second tile; each K/V tile then serves four heads, so a
-//    workgroup issues half the DMA per MFMA -- for chunks with enough row
-//    blocks (or split items) to fill the CUs anyway.
+// workgroup's wave64s are (query head hl) x (KV part kq), in one of three
+// shapes (template parameter P, chosen per chunk by the host):
+//  * P = 4, KV quarters (eight waves): each item runs as two workgroups, one
+//    per pair of the KV head's four GQA query heads; wave w owns the 32 rows
+//    {32 tokens} x {head 4*kvh + 2*hp + hl} and processes every fourth 32-key
+//    tile of the item (tiles kq, kq+4, ...).  A 512-token chunk fills the 256
+//    CUs.
+//  * P = 2, KV halves (eight waves): one workgroup holds all four heads of the
+//    group and every wave every second tile; each K/V tile then serves four
+//    heads, so a workgroup issues half the DMA per MFMA -- for chunks with
+//    enough row blocks (or split items) to fill the CUs anyway.
+//  * P = 1, KV whole (four waves): one wave per head of the group, every tile
+//    of the item; two workgroups share a CU, so a 2048-token chunk's 512
+//    workgroups run in one round, and there is no KV-part merge.
 // Each K/V tile staged in LDS is read by the waves of its part, and the parts
-// merge through LDS at the end.  Two waves per SIMD let one wave's softmax
-// run while the other's MFMAs occupy the matrix core.
+// merge through LDS at the end.  Two waves per SIMD (of one workgroup, or one
+// of each of two KV-whole workgroups) let one wave's softmax run while the
+// other's MFMAs occupy the matrix core.
 // The KV tiles of a row block are cut into splits of at most
 // `tiles_per_split` tiles (host-chosen for load balance: at least 768 keys,
 // no upper bound -- an item of any length runs in one workgroup), so only
@@ -114,8 +119,7 @@ typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 #define TM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
+constexpr int kMaxWaves = 8;  // waves of the largest workgroup shape
 
 // Phase clocks (diagnostic builds only, -DTRIANGLEMIX_PHASE_CLOCKS): lane 0 of
 // every wave stores the 100 MHz s_memrealtime clock at the TM_PHASE(slot)
@@ -125,12 +129,12 @@ constexpr int kThreads = kWaves * 64;
 #ifdef TRIANGLEMIX_PHASE_CLOCKS
 constexpr int kPhaseClockWorkgroups = 4096;
 constexpr int kPhaseClockSlots = 32;
-__device__ unsigned long long phase_clocks[kPhaseClockWorkgroups * kWaves * kPhaseClockSlots];
+__device__ unsigned long long phase_clocks[kPhaseClockWorkgroups * kMaxWaves * kPhaseClockSlots];
 #define TM_PHASE(slot)                                                                                   \
   do {                                                                                                   \
     const unsigned long long tm_clock_ = __builtin_amdgcn_s_memrealtime();                               \
     if ((threadIdx.x & 63) == 0 && blockIdx.x < kPhaseClockWorkgroups)                                   \
-      phase_clocks[(blockIdx.x * kWaves + (threadIdx.x >> 6)) * kPhaseClockSlots + (slot)] = tm_clock_; \
+      phase_clocks[(blockIdx.x * kMaxWaves + (threadIdx.x >> 6)) * kPhaseClockSlots + (slot)] = tm_clock_; \
   } while (0)
 #else
 #define TM_PHASE(slot) \
@@ -141,21 +145,29 @@ constexpr int kRowBytes = kHeadDim * 2;          // 256 B: one key row
 constexpr int kTileBytes = kKvTile * kRowBytes;  // 8 KB: K or V of one tile
 constexpr int kDmaPerTile = kTileBytes / 1024;   // 1 KB (4 key rows) per DMA instruction
 
-// Workgroup shape: the eight waves are kParts KV parts x kHeads query heads.
+// Workgroup shape: the waves are kParts KV parts x kHeads query heads.
 // P = 4 (two heads, KV quarters) puts a 512-token chunk's 16 row blocks on
 // 256 workgroups; P = 2 (all four heads of the GQA group, KV halves) loads
 // each K/V tile once for four heads and cuts an aligned sparse row block's 18
 // tiles into 9 + 9, for chunks with enough row blocks to fill the CUs.
+// P = 1 (KV whole: four waves, one per head of the group, every tile of the
+// item) has no KV-part merge and needs 64 KB of LDS, so two workgroups share
+// a CU (one wave of each per SIMD): a chunk of 64 row blocks runs its 512
+// workgroups in one round instead of two rounds of KV halves.
 template <int P>
 struct Shape {
   static constexpr int kParts = P;                      // KV parts: tiles kq, kq + P, ...
+  static constexpr int kWaves = P == 1 ? 4 : 8;         // waves per workgroup
+  static constexpr int kThreads = kWaves * 64;
   static constexpr int kHeads = kWaves / P;             // query heads per workgroup
   static constexpr int kWgPerKvHead = kGroup / kHeads;  // workgroups per (row block, KV head)
   static constexpr int kSlotBytes = P * kTileBytes;     // the tiles of all parts of one iteration
-  static constexpr int kDmaPerWave = 2 * P;             // DMA instructions per wave and iteration
-  static constexpr int kWavesPerTile = kDmaPerTile / kDmaPerWave;  // waves sharing one tile's DMA
+  static constexpr int kDmaPerWave = 2 * P * kDmaPerTile / kWaves;  // DMA instructions per wave and iteration
+  static constexpr int kWavesPerTile = kDmaPerTile / kDmaPerWave;   // waves sharing one tile's DMA
   static constexpr int kOwned = (kHeadDim / 32) / P;    // 32-wide d-blocks a wave keeps in the merge
-  static_assert((P == 4 || P == 2) && kHeads * P == kWaves, "supported shapes: 4 x 2 and 2 x 4");
+  static constexpr int kQBlocksPerWave = 8 * kHeads / kWaves;  // 1 KB blocks of Q each wave DMAs
+  static_assert((P == 4 || P == 2 || P == 1) && kHeads * P == kWaves && kHeads <= kGroup,
+                "supported shapes: 4 x 2, 2 x 4 and 1 x 4");
 };
 // Buffer-resource word 3 for raw (unformatted, stride 0) dword loads on gfx9.
 constexpr int kBufferFlags = 0x00020000;
@@ -330,8 +342,10 @@ __device__ __forceinline__ float softmax_update(float m_tile, float& m_run, floa
   return m_run == -INFINITY ? 0.0f : m_run;
 }
 
+// At least two waves per SIMD: the eight-wave shapes hold two by themselves,
+// and two KV-whole workgroups share a CU only within that register budget.
 template <bool kSparse, int P>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(Shape<P>::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query, int query_start, int seq_len,
                                 int num_row_blocks, int sparse_begin_arg, int sparse_end_arg, int split_items,
                                 int split_row_blocks, int tiles_per_split, KernelParams p) {
@@ -399,8 +413,8 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   // ---- DMA: per iteration the 2P tiles (K and V of every part) ----
   // A tile is eight wave-instructions of 1 KB (4 key rows).  With P = 4 wave w
   // loads one whole tile (waves 0-3 the K tile of quarter w, waves 4-7 the V
-  // tile of quarter w - 4); with P = 2 two waves share a tile, four
-  // instructions each.  Lane i of instruction j writes LDS slot (row 4j + i/16,
+  // tile of quarter w - 4); with P = 2 and P = 1 two waves share a tile, four
+  // instructions each (P = 1: waves 0-1 load K, 2-3 V).  Lane i of instruction j writes LDS slot (row 4j + i/16,
   // slot i%16), so it loads the global chunk the swizzle puts in that slot.
   const int dma_tile = wave / S::kWavesPerTile;
   const int dma_t = dma_tile / P;  // 0 = K, 1 = V
@@ -447,18 +461,19 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   int refill_phys = lane_page(2 * kTableTiles + lane);
   // ---- Q: the workgroup's H heads x 32 rows (8 KB per head), DMA'd once into LDS ----
   // (each of the P part waves of a head needs all of it; loading it per wave
-  // would multiply the start-up traffic through the CU).  Wave w loads the H
-  // 1 KB blocks g = H w .. H w + H - 1: head g / 8, rows 4 (g % 8) .. + 3;
-  // lane i writes slot i % 16 of row 4 (g % 8) + i / 16, i.e. global chunk
-  // k_slot(row, i % 16).  The range ends at the block's last row: rows past
-  // seq_len read 0.  Issued before the wait on the block table (no dependency).
+  // would multiply the start-up traffic through the CU).  Wave w loads the B =
+  // 8 H / waves 1 KB blocks g = B w .. B w + B - 1: head g / 8, rows 4 (g % 8)
+  // .. + 3; lane i writes slot i % 16 of row 4 (g % 8) + i / 16, i.e. global
+  // chunk k_slot(row, i % 16).  The range ends at the block's last row: rows
+  // past seq_len read 0.  Issued before the wait on the block table (no
+  // dependency).
   {
     const __amdgpu_buffer_rsrc_t q_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(pa.query + ((size_t)(tb - pa.query_start) * kQueryHeads + kvh * kGroup + H * hp) * kHeadDim),
         (short)0, (te - tb - 1) * kQueryHeads * kRowBytes + H * kRowBytes, kBufferFlags);
 #pragma unroll
-    for (int j = 0; j < H; ++j) {
-      const int g = H * wave + j;
+    for (int j = 0; j < S::kQBlocksPerWave; ++j) {
+      const int g = S::kQBlocksPerWave * wave + j;
       const int row = 4 * (g & 7) + (lane >> 4);
       const unsigned off = (unsigned)(row * kQueryHeads * kRowBytes + (g >> 3) * kRowBytes + 16 * k_slot(row, lane & 15));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(q_rsrc, TM_LDS(q_lds + g * 1024), 16, off, 0, 0, 0);
@@ -691,7 +706,7 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
     // back for block 2, so both reach the barrier at about the same time
     // (1-2 % faster per chunk; with KV quarters it measured neutral to 1 %
     // slower, so that shape keeps equal priorities).
-    if (P == 2 && wave >= kWaves / 2) __builtin_amdgcn_s_setprio(1);
+    if (P == 2 && wave >= S::kWaves / 2) __builtin_amdgcn_s_setprio(1);
     const int ti = P * it + kq;
     // Ragged last iteration: the parts without a tile idle; nothing is
     // left to prefetch in the last iteration.
@@ -851,13 +866,22 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   // v_free and xm / xl [hl][part][lane] live in q_lds; for P = 2 gi = 0 fills
   // q_lds, gi = 1 fills k_lds0 (waves 0-3) and k_lds1 (waves 4-7), and xm / xl
   // live in v_free.  kq is wave-uniform, so the per-block branches are scalar;
-  // the barrier stays outside them.
+  // the barrier stays outside them.  With P = 1 there is nothing to merge.
   if (num_iters == 0) {  // no iteration ran: the prologue DMA may still be landing
     wait_dma();
     __syncthreads();
   }
   char* v_free = (num_iters & 1) ? v_lds1 : v_lds0;  // the last iteration read v_lds((num_iters - 1) % 2)
   constexpr int O = S::kOwned;
+  // The merged (unnormalised) d-blocks kq * O + o.  Local arrays keep a fixed
+  // size (the largest shape's): hipcc's host pass drops a kernel template
+  // whose local arrays have a size that depends on the template parameters.
+  f32x16_t kept[kHeadDim / 32];
+  static_assert(O <= kHeadDim / 32 && P <= 4, "kept, mq and lq hold the largest shape's blocks");
+  if constexpr (P == 1) {
+#pragma unroll
+    for (int m = 0; m < kHeadDim / 32; ++m) kept[m] = o_acc[m];
+  } else {
   static_assert(P != 4 || H * P * 4 * 64 * 16 == S::kSlotBytes, "P = 4: one given block of all waves fills a slot");
   static_assert(P != 4 || 2 * H * P * 64 * 4 <= H * kRowBlock * kRowBytes, "P = 4: xm / xl fit in q_lds");
   static_assert(P != 2 || (H * P * 4 * 64 * 16 == H * kRowBlock * kRowBytes && 4 * 4 * 64 * 16 == S::kSlotBytes),
@@ -892,11 +916,6 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   xm[self * 64 + lane] = m_run;
   xl[self * 64 + lane] = l_run;
   __syncthreads();
-  // The merged (unnormalised) d-blocks kq * O + o.  Local arrays keep a fixed
-  // size (the largest shape's): hipcc's host pass drops a kernel template
-  // whose local arrays have a size that depends on the template parameters.
-  f32x16_t kept[kHeadDim / 32 / 2];
-  static_assert(O <= kHeadDim / 32 / 2 && P <= 4, "kept, mq and lq hold the largest shape's blocks");
   {
     float mq[4], lq[4];  // the first P are used
     float mt = -INFINITY;
@@ -932,6 +951,7 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
     l_run = lt;
     m_run = mt;
   }
+  }  // P > 1
 
   // The sc1 cache policy (agent scope): stores are written through to, and
   // loads served from, the level where every L2 of the GPU is coherent.  The
@@ -953,8 +973,8 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   constexpr int kStageRow = H * kRowBytes;
   constexpr int kChunksPerRow = kStageRow / 16;     // 32 (H = 2) or 64 (H = 4)
   constexpr int kRowsPerStore = 64 / kChunksPerRow;  // rows per store instruction: 2 or 1
-  constexpr int kStores = kRowBlock / (kRowsPerStore * kWaves);
-  static_assert(kRowsPerStore * kChunksPerRow == 64 && kStores * kRowsPerStore * kWaves == kRowBlock,
+  constexpr int kStores = kRowBlock / (kRowsPerStore * S::kWaves);
+  static_assert(kRowsPerStore * kChunksPerRow == 64 && kStores * kRowsPerStore * S::kWaves == kRowBlock,
                 "the stores cover the row block");
   auto store_rows = [&](const f32x16_t* blocks, float l_lane, char* stage) {
     const float l_tot = half_sum(l_lane);
@@ -986,7 +1006,9 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   };
   // Stage: KV quarters use the last iteration's V slot (its reads ended
   // before the merge barrier; 16 KB of its 32 KB); KV halves need 32 KB and
-  // use q_lds, whose merge reads must end first.
+  // use q_lds, whose merge reads must end first; KV whole uses q_lds too,
+  // whose only reads (the Q operand, before the first iteration) every wave
+  // finished before a barrier all waves have passed since.
   static_assert(kRowBlock * kStageRow <= (P == 4 ? S::kSlotBytes : H * kRowBlock * kRowBytes), "stage fits");
   char* const stage = P == 4 ? ((num_iters & 1) ? v_lds0 : v_lds1) : q_lds;
   TM_PHASE(13);
@@ -1080,14 +1102,16 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
   // loads in flight: a batch that raises the running max rescales what is
   // already summed (the online-softmax rule).  Slots past the last split
   // take this workgroup's own values again (registers, no load), weighted 0.
-  constexpr int kMergeBatch = 4;
-  f32x16_t acc[kHeadDim / 32 / 2];
+  // A KV-whole wave holds all four d-blocks, so it takes one split at a time
+  // (four would hold 256 more VGPRs).
+  constexpr int kMergeBatch = P == 1 ? 1 : 4;
+  f32x16_t acc[kHeadDim / 32];
 #pragma unroll
   for (int o = 0; o < O; ++o) acc[o] = f32x16_t{};
   float mt = -INFINITY, lt = 0.0f;
   for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
-    float ms[kMergeBatch], ls[kMergeBatch];
-    f32x4_t xs[kMergeBatch][kHeadDim / 32 / 2][4];
+    float ms[4], ls[4];  // fixed sizes (see kept); the first kMergeBatch are used
+    f32x4_t xs[4][kHeadDim / 32][4];
 #pragma unroll
     for (int b = 0; b < kMergeBatch; ++b) {
       const int sb = s0 + b;
@@ -1152,13 +1176,15 @@ triangle_paged_attention_kernel(const int32_t* block_table, const __bf16* query,
 template <bool kSparse, int P>
 hipError_t launch(const KernelParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((triangle_paged_attention_kernel<kSparse, P>),
-                     dim3((unsigned)(p.items_per_head * Shape<P>::kWgPerKvHead * kKvHeads)), dim3(kThreads), 0,
+                     dim3((unsigned)(p.items_per_head * Shape<P>::kWgPerKvHead * kKvHeads)),
+                     dim3(Shape<P>::kThreads), 0,
                      stream, p.block_table, p.query, p.query_start, p.seq_len, p.num_row_blocks, p.sparse_begin,
                      p.sparse_end, p.split_items, p.split_row_blocks, p.tiles_per_split, p);
   return hipGetLastError();
 }
 
 hipError_t launch_triangle_paged_attention(const KernelParams& p, bool sparse, int kv_parts, hipStream_t stream) {
+  if (kv_parts == 1) return sparse ? launch<true, 1>(p, stream) : launch<false, 1>(p, stream);
   if (kv_parts == 2) return sparse ? launch<true, 2>(p, stream) : launch<false, 2>(p, stream);
   return sparse ? launch<true, 4>(p, stream) : launch<false, 4>(p, stream);
 }

@@ -267,7 +267,7 @@ def test_workspace_size_agrees_with_the_launch_over_a_grid(lib):
                 assert lib.tm_last_error().decode() == size_msg
                 continue
             assert need <= MAX_WORKSPACE
-            assert _items(need) <= items.value and tiles.value >= 1 and parts.value in (2, 4)
+            assert _items(need) <= items.value and tiles.value >= 1 and parts.value in (1, 2, 4)
             if need > 0:
                 assert launch() == 3 and "smaller than" in lib.tm_last_error().decode()
                 assert launch(ws=OUT, ws_bytes=need) == 3 and "overlap" in lib.tm_last_error().decode()
@@ -396,6 +396,11 @@ BASELINE_PLANS = [
     ((7680, 512, 8192, 8192), (4, 124, 24)),       # config 2, last chunk: quarters in 1.5 rounds (31.3 us)
     ((4096, 512, 4608, 8192), (4, 32, 16)),        # config 2, a middle chunk: one item per row block, no split
     ((6272, 2048, 8320, 8320), (2, 128, 72)),      # config 3
+    ((2048, 2048, 4096, 8320), (1, 32, 64)),       # config 3, a middle chunk: KV whole, 512 workgroups in one round
+    ((0, 2048, 2048, 8320), (1, 32, 64)),          # config 3, the first chunk (dense rows of at most 17 tiles)
+    ((14336, 2048, 16384, 32768), (1, 32, 64)),    # config 4, a middle chunk at L = 32768
+    ((0, 2048, 2048, 2048), (2, 128, 64)),         # a whole 2048-token prompt: its 64-tile dense tail favours halves
+    ((8192, 1024, 9216, 32768), (2, 32, 32)),      # 32 row blocks: too few for two KV-whole workgroups per CU
     ((8192, 128, 8320, 8320), (4, 84, 16)),        # config 3, last chunk
     ((30720, 2048, 32768, 32768), (2, 128, 92)),   # config 4, last chunk at L = 32768
     ((129024, 2048, 131072, 131072), (2, 512, 92)),  # config 4, last chunk at L = 131072: tail rows in 8 pieces
