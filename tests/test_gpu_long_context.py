@@ -14,7 +14,9 @@ fp32 oracle runs on the GPU in its blocked form, so whole chunks are checked.
   prompt's last chunk and of a middle chunk, for the TriangleMix op, and of
   the dense companion's last chunk; tolerances as everywhere (max-abs 2e-2,
   mean-abs 2e-3, rel-L2 2e-2), the mean also per 32-row block.
-* The exact mask identity over the WHOLE last chunk: Q = 0 weighs every
+* The exact mask identity over the WHOLE last chunk (KV halves) and a whole
+  middle chunk at L = 32768 (KV whole: four-wave workgroups, two per CU,
+  one wave per head over every tile): Q = 0 weighs every
   attended key 1/|S|, and one-hot residue V rows turn each output row into
   the residue histogram of its key set (8 moduli), so one added, dropped or
   shifted key of any row changes the output.  Counts and sums are exact
@@ -69,8 +71,11 @@ def test_long_context_rows_match_oracle(gpu, L):
     for label, qs in (("last", L - CHUNK), ("middle", L // 2)):
         seq = qs + CHUNK
         qd = make_query(CHUNK, 900 + qs // 1024, std=1.0).to(gpu)
-        print(f"L={L} {label} chunk qs={qs} plan={cabi.chunk_plan(CHUNK, qs, seq, prompt)} "
+        plan = cabi.chunk_plan(CHUNK, qs, seq, prompt)
+        print(f"L={L} {label} chunk qs={qs} plan={plan} "
               f"workspace={cabi.workspace_size(CHUNK, qs, seq, prompt)}", flush=True)
+        # the middle chunk runs as KV whole (four-wave workgroups, two per CU), the last as KV halves
+        assert plan[0] == (1 if label == "middle" else 2), plan
         got = _sparse(gpu, qd, kd, vd, btd, qs, seq, prompt)
         _check_all_rows(f"L={L} {label} rows {qs}..{seq - 1}", got, qd, kd, vd, btd, qs, seq, prompt)
     assert cabi.workspace_size(CHUNK, L - CHUNK, L, prompt) > cabi.WORKSPACE_COUNTER_BYTES  # dense tail split
@@ -104,9 +109,13 @@ def _residue_histogram(intervals, m):
     return hist
 
 
-@pytest.mark.parametrize("L", [32768, 131072])
-def test_long_context_mask_identity_whole_last_chunk(gpu, L):
-    qs, seq, prompt = L - CHUNK, L, L
+@pytest.mark.parametrize("L,where", [(32768, "last"), (131072, "last"), (32768, "middle")])
+def test_long_context_mask_identity_whole_chunk(gpu, L, where):
+    """Every row of a 2048-row chunk: the last one (KV halves, dense-tail rows split over KV) and a middle
+    one (KV whole)."""
+    qs = L - CHUNK if where == "last" else L // 2
+    seq, prompt = qs + CHUNK, L
+    print(f"mask identity L={L} {where} chunk qs={qs} plan={cabi.chunk_plan(CHUNK, qs, seq, prompt)}", flush=True)
     _, _, bt = make_cache(L, 800 + L // 1024)
     pages = int(bt.max()) + 1
     moduli = [128, 127, 125, 123, 121, 119, 113, 109]
