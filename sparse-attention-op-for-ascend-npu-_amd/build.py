@@ -10,6 +10,9 @@ Usage: ``python build.py [--hip-only]``.  Each call recompiles.
 ``python build.py --phase-clocks`` builds the diagnostic phase-clock library
 ``trianglemix/libtrianglemix_phase_clocks.so`` instead: a diagnostic build whose kernels store
 per-wave ``s_memrealtime`` clocks at phase boundaries (exports ``tm_phase_clocks_read`` / ``_clear``).
+``python build.py --plan-override`` builds ``trianglemix/libtrianglemix_plan_override.so``: the product
+library plus a ``tm_plan_override(kv_parts, tiles_per_split)`` export that forces every call's launch plan,
+for the forced-plan sweep the planner's costs are fitted to (``tests/plan_sweep.py``).
 """
 
 from __future__ import annotations
@@ -31,6 +34,7 @@ ARCH = "gfx950"
 
 HIP_LIB = PKG / "libtrianglemix.so"
 PHASE_CLOCK_LIB = PKG / "libtrianglemix_phase_clocks.so"  # diagnostic build (--phase-clocks), not loaded by the op
+PLAN_OVERRIDE_LIB = PKG / "libtrianglemix_plan_override.so"  # diagnostic build (--plan-override), not loaded by the op
 TORCH_LIB = PKG / "_trianglemix_torch.so"
 
 # Disable packed fp32 VALU ops in device code: some of their forms have given
@@ -73,13 +77,15 @@ def _atomic_replace(tmp: Path, dst: Path) -> None:
     os.replace(tmp, dst)
 
 
-def build_hip_library(phase_clocks: bool = False) -> Path:
+def build_hip_library(phase_clocks: bool = False, plan_override: bool = False) -> Path:
     """The kernels + C ABI; ``phase_clocks`` builds the diagnostic variant that records per-wave phase clocks
-    (read back through its ``tm_phase_clocks_read`` export) into its own file."""
+    (read back through its ``tm_phase_clocks_read`` export), ``plan_override`` the one whose
+    ``tm_plan_override`` export forces the launch plan, each into its own file."""
     hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
-    dst = PHASE_CLOCK_LIB if phase_clocks else HIP_LIB
+    dst = PHASE_CLOCK_LIB if phase_clocks else (PLAN_OVERRIDE_LIB if plan_override else HIP_LIB)
     tmp = dst.with_suffix(".so.tmp")
-    _run([hipcc, *HIP_FLAGS, *(["-DTRIANGLEMIX_PHASE_CLOCKS"] if phase_clocks else []), "-shared", f"-I{INCLUDE}",
+    defines = (["-DTRIANGLEMIX_PHASE_CLOCKS"] if phase_clocks else []) + (["-DTRIANGLEMIX_PLAN_OVERRIDE"] if plan_override else [])
+    _run([hipcc, *HIP_FLAGS, *defines, "-shared", f"-I{INCLUDE}",
           str(CSRC / "trianglemix_kernel.hip"), str(CSRC / "trianglemix_cache.hip"), str(CSRC / "trianglemix_capi.cpp"),
           "-o", str(tmp)])
     _atomic_replace(tmp, dst)
@@ -120,9 +126,14 @@ def main() -> int:
     ap.add_argument("--hip-only", action="store_true")
     ap.add_argument("--phase-clocks", action="store_true",
                     help="build only the diagnostic phase-clock library (libtrianglemix_phase_clocks.so)")
+    ap.add_argument("--plan-override", action="store_true",
+                    help="build only the diagnostic plan-override library (libtrianglemix_plan_override.so)")
     args = ap.parse_args()
     if args.phase_clocks:
         print(f"built {build_hip_library(phase_clocks=True)}")
+        return 0
+    if args.plan_override:
+        print(f"built {build_hip_library(plan_override=True)}")
         return 0
     for p in build_all(args.hip_only):
         print(f"built {p}")

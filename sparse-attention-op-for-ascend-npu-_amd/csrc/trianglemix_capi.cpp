@@ -65,106 +65,87 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
   return TM_OK;
 }
 
-// Workgroup shape.  KV quarters: two query heads per workgroup over four KV
-// parts, 16 workgroups per work item.  KV halves: the four heads of a GQA
-// group over two KV parts, 8 workgroups per item; each K/V tile then serves
-// four heads and a workgroup issues half the DMA and merge work per MFMA.
-// Halves run every chunk of more than 16 row blocks (16 x row blocks quarter
-// workgroups would exceed the 256 CUs, 8 x row blocks halves ones do not up
-// to 32).  Below that, a TriangleMix chunk takes the shape whose simulated
-// plan is shorter (see the costs below); a dense-companion chunk of at least
-// 4 row blocks runs as halves when their plan splits a row block over KV and
-// the chunk holds at least kHalvesDenseMinTiles tiles per KV head, as
-// quarters otherwise.  Measured on MI355X:
-//  * unsplit chunks of up to 16 row blocks run 15-25 % faster as quarters
-//    (the simulation agrees: half the iterations per item);
-//  * dense-companion chunks of up to 16 row blocks, whose rows all split, run
-//    faster as halves only with enough work: over whole prefills in chunks of
-//    128-512 (L = 4096-16384) the tile bound is the fastest rule or within
-//    1 % of it, against up to 9 % slower for halves on every split chunk and
-//    up to 12 % slower for quarters on every one.
+// Workgroup shapes.  KV quarters (P = 4): two query heads per workgroup over
+// four KV parts, 16 workgroups per work item, one per CU.  KV halves (P = 2):
+// the four heads of a GQA group over two KV parts, 8 workgroups per item, one
+// per CU; each K/V tile then serves four heads.  KV whole (P = 1): four waves,
+// one per head, over every tile of the item, 8 workgroups per item, two per
+// CU; no KV-part merge.  Per KV head the 256 CUs hold 16 quarters, 32 halves
+// or 64 KV-whole workgroups at once: a shape's slots.
 //
-// KV whole (four waves, one per head, every tile of the item; two workgroups
-// per CU) takes a TriangleMix chunk of at least kWholeMinRowBlocks row blocks
-// whose KV-halves plan splits no row block, when its simulated makespan
-// (below) is the shorter: a chunk of 64 sparse row blocks then fills the CUs
-// in one round where KV halves run two, and no KV-part merge remains; a chunk
-// holding long rows (a short prompt's dense tail) stays with KV halves, whose
-// waves take half of every such row.
-// Measured on MI355X (eager, one box): sparse middle chunks of 1536, 2048,
-// 3072 and 4096 rows 16 %, 12 %, 5 % and 12 % faster than KV halves, the
-// 2048-row chunks of an 8320- or 32768-token prompt 12-18 %; 1024-row chunks
-// (256 workgroups, one per CU) 15 % slower, a whole 2048-token prompt (its
-// 64-tile dense tail in one wave per row block) 17 % slower, chunks whose
-// dense tail splits 1-36 % slower (each split piece then runs all its tiles in
-// one wave), and so are most of the dense companion's chunks (their rows
-// split).
-constexpr int kHalvesMinRowBlocks = 17;
+// A plan is a shape and T, the most tiles an item takes: a row block of n
+// tiles is cut into ceil(n / T) near-equal items (an item may hold any number
+// of tiles, so rows split only for load balance).  A plan is costed by
+// simulating the greedy dispatch of its items, issued heaviest row block first
+// as the grid lists them, each onto the least loaded slot.  An item costs a
+// fixed part (start-up, KV-part merge, output store) plus a part per loop
+// iteration (ceil(tiles / P) iterations).  A split row block completes when
+// its last piece has finished plus the in-launch merge: a fixed part and a
+// part per piece, whose partials the last arriving workgroup reads back.  The
+// plan's time is its latest slot or split row block.  The candidate with the
+// shortest simulated time is taken (ties: the larger T, fewer partials).
+//
+// Three regimes, with costs fitted on MI355X to sweeps of forced plans (every
+// candidate plan of each geometry timed as 20 launches, fastest of three
+// passes, HIP events): 87 TriangleMix and dense-companion chunks of 64 to
+// 12288 rows at prompts of 1024 to 131072 tokens, 35 of them held out of the
+// first fit to check it.  The fit minimised the time the planned plans lose
+// to each geometry's fastest measured plan.  Summed over the 87 chunks the
+// planned plans lose 46 us of 6,479 us (0.7 %); charging the merge to the
+// whole chunk instead of the split rows, with the earlier costs and candidate
+// rules, lost 189 us.
+//  * TriangleMix chunks of up to 16 row blocks: quarters (T from the ladder,
+//    32-128 tiles) or halves (T of 24 tiles and more).  Quarters stay on the
+//    ladder: their longer items move twice the K/V of halves ones per head.
+//    Config 1's chunk: quarters over 84-tile items, 17.9 us (halves over
+//    28-tile items: 19.1 us).
+//  * Chunks of 17 row blocks or more, TriangleMix and dense companion:
+//    halves or KV whole, T of 16 tiles and more.  KV whole fills the GPU
+//    with two workgroups per CU, pays no KV-part merge, and split into pieces
+//    it also serves the long dense-tail rows of a prompt's last chunks: the
+//    last 2048 rows of a 131072-token prompt take 311 us as KV whole over
+//    256-tile pieces against 346 us as halves over 512-tile ones.
+//  * Dense-companion chunks of up to 16 row blocks: halves when their plan
+//    splits a row block and the chunk holds at least kHalvesDenseMinTiles
+//    tiles per KV head, quarters otherwise (over whole dense prefills in
+//    chunks of 128-512 at L = 4096-16384 the fastest rule, or within 1 % of
+//    it), each with the T its simulation picks.
+// A candidate is taken only if its split row blocks' counters and partials
+// fit the workspace bound (tmx::kMaxSplitRowBlocks, tmx::kMaxSplitItems); the
+// no-split plan always does, so every chunk has a plan.
+struct PlanModel {
+  int slots;               // workgroups of one KV head resident at once
+  int parts;               // KV parts: tiles per workgroup and loop iteration
+  double item_fixed;       // an item's fixed part ...
+  double per_iteration;    // ... plus this much per loop iteration
+  double merge_fixed;      // a split row block's merge ...
+  double merge_per_piece;  // ... plus this much per piece
+};
+// Relative costs (only their ratios matter).
+constexpr PlanModel kSmallQuarters{16, 4, 5.351, 1.239, 0.040, 0.749};
+constexpr PlanModel kSmallHalves{32, 2, 8.112, 0.841, 2.298, 1.084};
+constexpr PlanModel kLargeHalves{32, 2, 5.307, 0.483, 0.875, 1.489};
+constexpr PlanModel kLargeWhole{64, 1, 4.908, 0.456, 0.555, 1.027};
+constexpr PlanModel kDenseQuarters{16, 4, 6, 1, 1, 1};
+constexpr PlanModel kDenseHalves{32, 2, 5, 1, 3, 1};
+constexpr int kMaxSlots = 64;
+static_assert(kSmallQuarters.slots <= kMaxSlots && kSmallHalves.slots <= kMaxSlots &&
+                  kLargeHalves.slots <= kMaxSlots && kLargeWhole.slots <= kMaxSlots &&
+                  kDenseQuarters.slots <= kMaxSlots && kDenseHalves.slots <= kMaxSlots,
+              "simulated_time's slot heap");
+constexpr int kLargeMinRowBlocks = 17;
 constexpr int kHalvesSplitMinRowBlocks = 4;
 constexpr int64_t kHalvesDenseMinTiles = 2048;
-constexpr int kWholeMinRowBlocks = 48;
-
-// Split-KV sizing and shape choice.  A work item runs as 16 (KV quarters) or
-// 8 (KV halves) workgroups, one per CU, so each of the item's workgroup
-// positions has slots = 256 / that many CUs.  A row block of n tiles is cut
-// into ceil(n / T) near-equal items of at most T tiles.  A plan is costed by
-// simulating the greedy dispatch of its items (issued heaviest row block
-// first) onto the slots, in loop iterations: an item costs a fixed start-up +
-// store part plus ceil(tiles / parts) iterations (a workgroup runs one tile
-// per KV part and iteration), and a plan that splits anything pays for the
-// in-launch merge -- a fixed part plus one iteration per piece of its most
-// split row block, whose last arriving workgroup reads every partial back.
-// T is the candidate with the shortest makespan (ties: larger T, fewer
-// partials).  TriangleMix chunks of up to 16 row blocks take the shape whose
-// best plan has the shorter makespan.
-//
-// The costs are fitted to a forced-(shape, T) sweep on MI355X (every plan
-// timed after a clock warm-up, in forward, reverse and forward order) of 30
-// chunks: 21 TriangleMix ones (96-2048 rows at the end of 2560-32768-token
-// prompts) and 9 dense-companion ones.  At the fit the planned plan was the
-// fastest measured on 26 of them and at most 2.3 us slower on the rest, 4.4
-// us summed against 18.3 for the previous costs (which kept quarters to one
-// round of workgroups and charged every split item for the merge).  Quarters
-// take the last 512-row chunk of 3584- to 12288-token prompts in up to 1.5
-// rounds: 31.3 us against 32.0 as halves at L = 8192.  Re-swept after the
-// kernel's output store changed: within 0.3 us of the fastest on 24 chunks,
-// 3.3 us behind at worst and 9.3 us in sum (0.8 % of the chunks' time); an
-// integer refit would save 1.7 us of that but move config 1's chunk to a plan
-// measured 0.17 us slower, so the costs stay.
-// T is at least kMinSplitTiles (1024 keys: a split's fp32 partial of 66 KB
-// stays small next to the K/V it reads, 16 KB per 32-key tile); KV-halves
-// plans of TriangleMix chunks of at most 16 row blocks may go down to
-// kFineSplitTiles (768 keys), one more piece per dense-tail row while the
-// items still fit the slots (2-4 % faster on the last 384-512 rows of
-// 2560-4992-token prompts).  The candidates are the ladder kLadderTop,
-// kLadderTop - 4, ... down to that floor (the costs above were fitted on it)
-// and, for rows longer than kLadderTop tiles, every T that cuts the longest
-// row into whole pieces above the ladder, down to one piece (no split).  An
-// item may hold any number of tiles, so rows split for load balance only.
-// A candidate is taken only if its split row blocks' counters and partials
-// fit the workspace bound (tmx::kMaxSplitRowBlocks, tmx::kMaxSplitItems);
-// the no-split plan always does, so every chunk has a plan.
-struct PlanCosts {
-  int slots;
-  int parts;            // KV parts: tiles per workgroup and iteration
-  int item_fixed;       // start-up and store of an item, in iterations
-  int merge_fixed;      // the in-launch merge of a split row block, in iterations ...
-  int merge_per_piece;  // ... plus this many per piece of the most split row block
-};
-constexpr PlanCosts kQuarterCosts{16, 4, 6, 1, 1};
-constexpr PlanCosts kHalfCosts{32, 2, 5, 3, 1};
-// KV whole: 8 workgroups per item, two per CU, one tile per iteration.  Only
-// plans without a split are costed for it (see choose_plan).
-constexpr PlanCosts kWholeCosts{64, 1, 5, 3, 1};
-constexpr int kMaxSlots = 64;
-static_assert(kQuarterCosts.slots <= kMaxSlots && kHalfCosts.slots <= kMaxSlots && kWholeCosts.slots <= kMaxSlots,
-              "simulated_makespan's slot heap");
+// Smallest T per regime: 1024 keys (quarters, dense companion), 768 keys
+// (halves of small TriangleMix chunks), 512 keys (chunks of 17+ row blocks).
 constexpr int kMinSplitTiles = 1024 / tmx::kKvTile;
 constexpr int kFineSplitTiles = 768 / tmx::kKvTile;
-// Beyond this many items per candidate the simulation is skipped (its host
-// cost would show): T then spreads the chunk's tiles over one item per slot.
+constexpr int kLargeSplitTiles = 512 / tmx::kKvTile;
+// A chunk of more than this many items at T = kMinSplitTiles is not
+// simulated (its host cost would show): T then spreads the chunk's tiles over
+// one KV-halves item per slot.
 constexpr int64_t kMaxSimulatedItems = 4096;
-constexpr int kLadderTop = 128;  // candidate T: kLadderTop, kLadderTop - 4, ..., >= the floor
+constexpr int kLadderTop = 128;  // candidate T: kLadderTop, kLadderTop - 4, ..., down to the floor
 constexpr int kSplitStep = 4;
 
 // The row blocks (in issue order, row_tiles[o] tiles each) up to the last one
@@ -195,40 +176,45 @@ bool layout_fits(const SplitLayout& s) {
   return s.split_row_blocks <= tmx::kMaxSplitRowBlocks && s.split_items <= tmx::kMaxSplitItems;
 }
 
-// Greedy dispatch of the items (issue order) onto the slots, each to the
-// least loaded one (a min-heap of slot loads), in loop iterations.
-int64_t simulated_makespan(const std::vector<int>& row_tiles, int T, const PlanCosts& c) {
-  int64_t heap[kMaxSlots] = {};  // all zero: a valid min-heap
-  auto add_to_least = [&](int64_t cost) {
-    int64_t v = heap[0] + cost;  // replace the root, sift down
+// The simulated time of a plan (see above): a min-heap of slot loads.
+double simulated_time(const std::vector<int>& row_tiles, int T, const PlanModel& m) {
+  double heap[kMaxSlots] = {};  // all zero: a valid min-heap
+  auto add_to_least = [&](double cost) {
+    const double v = heap[0] + cost;  // replace the root, sift down
     int i = 0;
     for (;;) {
       const int l = 2 * i + 1, r = l + 1;
-      int m = i;
-      int64_t mv = v;
-      if (l < c.slots && heap[l] < mv) m = l, mv = heap[l];
-      if (r < c.slots && heap[r] < mv) m = r, mv = heap[r];
-      if (m == i) break;
-      heap[i] = heap[m];
-      i = m;
+      int k = i;
+      double kv = v;
+      if (l < m.slots && heap[l] < kv) k = l, kv = heap[l];
+      if (r < m.slots && heap[r] < kv) k = r, kv = heap[r];
+      if (k == i) break;
+      heap[i] = heap[k];
+      i = k;
     }
     heap[i] = v;
+    return v;
   };
-  int most_pieces = 1;
+  double merged = 0.0;  // the latest split row block's merge
   for (const int n : row_tiles) {
     const int pieces = (n + T - 1) / T;
-    most_pieces = pieces > most_pieces ? pieces : most_pieces;
+    double last = 0.0;
     for (int i = 0; i < pieces; ++i) {
       const int size = (int)((int64_t)(i + 1) * n / pieces - (int64_t)i * n / pieces);
-      add_to_least(c.item_fixed + (size + c.parts - 1) / c.parts);
+      const double cost = m.item_fixed + m.per_iteration * (double)((size + m.parts - 1) / m.parts);
+      last = std::max(last, add_to_least(cost));
     }
+    if (pieces > 1) merged = std::max(merged, last + m.merge_fixed + m.merge_per_piece * pieces);
   }
-  int64_t makespan = 0;
-  for (int k = 0; k < c.slots; ++k) makespan = heap[k] > makespan ? heap[k] : makespan;
-  return makespan + (most_pieces > 1 ? c.merge_fixed + int64_t(c.merge_per_piece) * most_pieces : 0);
+  double end = merged;
+  for (int k = 0; k < m.slots; ++k) end = std::max(end, heap[k]);
+  return end;
 }
 
-// Candidate T, largest first (see above); ladder_only keeps T <= kLadderTop.
+// Candidate T, largest first: for rows longer than kLadderTop tiles every T
+// that cuts the longest row into whole pieces above the ladder (down to one
+// piece, no split) unless ladder_only, then the ladder kLadderTop,
+// kLadderTop - 4, ... down to min_tiles.
 std::vector<int> split_candidates(int longest, int min_tiles, bool ladder_only) {
   std::vector<int> t;
   if (longest > kLadderTop && !ladder_only) {
@@ -242,48 +228,85 @@ std::vector<int> split_candidates(int longest, int min_tiles, bool ladder_only) 
   return t;
 }
 
-struct SplitChoice {
-  int tiles_per_split;
-  int64_t makespan;  // in iterations; -1 when the simulation was skipped or no candidate fits
+struct ChunkPlan {
+  int kv_parts, tiles_per_split;
 };
 
-SplitChoice choose_tiles_per_split(const std::vector<int>& row_tiles, const PlanCosts& c,
-                                   int min_tiles = kMinSplitTiles, bool ladder_only = false) {
+// The best (shape, T) among the shapes' candidates, in the order given
+// (earlier shapes and larger T win ties); nullopt-like {0, 0} when none fits.
+struct ShapeCandidates {
+  int kv_parts;
+  const PlanModel* model;
+  int min_tiles;
+  bool ladder_only;
+};
+
+ChunkPlan best_plan(const std::vector<int>& row_tiles, std::initializer_list<ShapeCandidates> shapes) {
+  int longest = 0;
+  for (const int n : row_tiles) longest = std::max(longest, n);
+  ChunkPlan best{0, 0};
+  double best_time = 0.0;
+  for (const ShapeCandidates& s : shapes) {
+    bool unsplit_done = false;  // every T >= longest is the same plan: simulate the first only
+    for (const int tk : split_candidates(longest, s.min_tiles, s.ladder_only)) {
+      if (tk >= longest) {
+        if (unsplit_done) continue;
+        unsplit_done = true;
+      }
+      if (!layout_fits(split_layout(row_tiles, tk))) continue;
+      const double t = simulated_time(row_tiles, tk, *s.model);
+      if (best.kv_parts == 0 || t < best_time) {
+        best = {s.kv_parts, tk};
+        best_time = t;
+      }
+    }
+  }
+  return best;
+}
+
+ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
+  const int num_row_blocks = (int)row_tiles.size();
   int64_t total = 0;
   int longest = 0;
   for (const int n : row_tiles) {
     total += n;
-    longest = n > longest ? n : longest;
+    longest = std::max(longest, n);
   }
-  if (longest <= min_tiles) return {min_tiles, simulated_makespan(row_tiles, min_tiles, c)};  // nothing to split
-  const std::vector<int> cands = split_candidates(longest, min_tiles, ladder_only);
-  if (total / min_tiles > kMaxSimulatedItems) {
-    // Spread the tiles over one item per slot; the largest candidate that
-    // does not go below that and fits the workspace bound (one piece always
-    // does).  Such chunks have so many row blocks that this rarely splits.
-    const int64_t per_item = (total + c.slots - 1) / c.slots;
+  if (total / kMinSplitTiles > kMaxSimulatedItems) {
+    // Spread the tiles over one KV-halves item per slot: the largest
+    // candidate that does not go below that share and fits the workspace
+    // bound (one piece always does).  Such chunks have so many row blocks, or
+    // rows so long, that this rarely splits.
+    const int64_t per_item = (total + kLargeHalves.slots - 1) / kLargeHalves.slots;
+    const std::vector<int> cands = split_candidates(longest, kMinSplitTiles, false);
     int pick = cands.front();
     for (const int tk : cands) {
       if (tk < per_item || !layout_fits(split_layout(row_tiles, tk))) break;
       pick = tk;
     }
-    return {pick, -1};
+    return {2, pick};
   }
-  int best_t = 0;
-  int64_t best = -1;
-  for (const int tk : cands) {
-    if (!layout_fits(split_layout(row_tiles, tk))) continue;
-    const int64_t ms = simulated_makespan(row_tiles, tk, c);
-    if (best < 0 || ms < best) {  // ties keep the larger T (fewer partials)
-      best = ms;
-      best_t = tk;
-    }
+  if (num_row_blocks >= kLargeMinRowBlocks) {
+    return best_plan(row_tiles, {{2, &kLargeHalves, kLargeSplitTiles, false},
+                                 {1, &kLargeWhole, kLargeSplitTiles, false}});
   }
-  return {best_t, best};
+  if (sparse) {
+    return best_plan(row_tiles, {{4, &kSmallQuarters, kMinSplitTiles, true},
+                                 {2, &kSmallHalves, kFineSplitTiles, false}});
+  }
+  const ChunkPlan halves = best_plan(row_tiles, {{2, &kDenseHalves, kMinSplitTiles, false}});
+  if (num_row_blocks >= kHalvesSplitMinRowBlocks && longest > halves.tiles_per_split &&
+      total >= kHalvesDenseMinTiles) {
+    return halves;
+  }
+  return best_plan(row_tiles, {{4, &kDenseQuarters, kMinSplitTiles, false}});
 }
 
 // The choice depends only on the chunk geometry, which repeats for every layer
-// of a step: a small per-thread cache keeps the simulation off the launch path.
+// of a step: a per-thread cache keeps the simulation (10-250 us on the host)
+// off the launch path.  64 entries hold every chunk of a 131072-token prefill
+// in chunks of 2048, so even a sequence of distinct chunks repeated layer by
+// layer plans each chunk once.
 struct PlanKey {
   int64_t num_row_blocks, query_start, seq_len, sparse_begin, sparse_end;
   bool operator==(const PlanKey& o) const {
@@ -292,55 +315,19 @@ struct PlanKey {
   }
 };
 
-struct ChunkPlan {
-  int kv_parts, tiles_per_split;
-};
-
-ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
-  const int num_row_blocks = (int)row_tiles.size();
-  if (num_row_blocks >= kHalvesMinRowBlocks) {
-    const SplitChoice halves = choose_tiles_per_split(row_tiles, kHalfCosts);
-    const int t = halves.tiles_per_split;
-    if (sparse && num_row_blocks >= kWholeMinRowBlocks && halves.makespan >= 0 &&
-        split_layout(row_tiles, t).split_row_blocks == 0 &&
-        simulated_makespan(row_tiles, t, kWholeCosts) < halves.makespan) {
-      return {1, t};
-    }
-    return {2, t};
-  }
-  if (sparse) {
-    // TriangleMix: the shape whose best plan has the shorter makespan.
-    // Quarters take items of at most kLadderTop tiles here: with longer
-    // items the model, whose costs count a quarters iteration like a halves
-    // one although it moves twice the K/V, prefers quarters where halves
-    // measure faster (the last 512 rows of a 32768-token prompt: quarters
-    // over 256-tile items 92.1 us, halves over 147-tile items 85.6 us).
-    // Without a fitting quarters plan (rows too long for the workspace
-    // bound), halves run.
-    const SplitChoice quarters = choose_tiles_per_split(row_tiles, kQuarterCosts, kMinSplitTiles, true);
-    const SplitChoice halves = choose_tiles_per_split(row_tiles, kHalfCosts, kFineSplitTiles);
-    const bool use_halves = halves.makespan >= 0 && quarters.makespan >= 0 ? halves.makespan < quarters.makespan
-                                                                           : quarters.makespan < 0;
-    return use_halves ? ChunkPlan{2, halves.tiles_per_split} : ChunkPlan{4, quarters.tiles_per_split};
-  }
-  const SplitChoice quarters = choose_tiles_per_split(row_tiles, kQuarterCosts);
-  // Dense companion: halves when their plan splits a row block and the chunk
-  // holds at least kHalvesDenseMinTiles tiles per KV head (the measured rule).
-  const int t_halves = choose_tiles_per_split(row_tiles, kHalfCosts).tiles_per_split;
-  if (num_row_blocks >= kHalvesSplitMinRowBlocks) {
-    int64_t total = 0;
-    bool split = false;
-    for (const int n : row_tiles) {
-      total += n;
-      split = split || n > t_halves;
-    }
-    if (split && total >= kHalvesDenseMinTiles) return {2, t_halves};
-  }
-  return {4, quarters.tiles_per_split};
-}
+#ifdef TRIANGLEMIX_PLAN_OVERRIDE
+// Diagnostic builds only (-DTRIANGLEMIX_PLAN_OVERRIDE): a plan that every
+// call takes instead of the planner's, for the forced-plan sweeps the costs
+// above are fitted to.  Not thread-safe; the product library is built without
+// it.
+int g_override_parts = 0, g_override_tiles = 0;
+#endif
 
 ChunkPlan cached_plan(const PlanKey& key) {
-  constexpr int kEntries = 8;
+#ifdef TRIANGLEMIX_PLAN_OVERRIDE
+  if (g_override_parts > 0) return ChunkPlan{g_override_parts, g_override_tiles};
+#endif
+  constexpr int kEntries = 64;
   thread_local PlanKey keys[kEntries];
   thread_local ChunkPlan values[kEntries];
   thread_local int used = 0, next = 0;
@@ -637,6 +624,17 @@ int tm_chunk_plan(int dense, int64_t query_tokens, int64_t query_start, int64_t 
   *items_per_kv_head = g.items_per_head;
   return TM_OK;
 }
+
+#ifdef TRIANGLEMIX_PLAN_OVERRIDE
+// Diagnostic export: every later call takes (kv_parts, tiles_per_split) as
+// its plan; kv_parts 0 returns to the planner.  Calls the planner would not
+// make (a layout beyond the workspace bound) are still refused.
+void tm_plan_override(int32_t kv_parts, int32_t tiles_per_split) {
+  const bool valid = (kv_parts == 1 || kv_parts == 2 || kv_parts == 4) && tiles_per_split > 0;
+  g_override_parts = valid ? kv_parts : 0;
+  g_override_tiles = valid ? tiles_per_split : 0;
+}
+#endif
 
 int tm_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
                          const int64_t* slot_mapping, int64_t num_tokens, int64_t key_stride, int64_t value_stride,

@@ -138,10 +138,9 @@ def test_whole_prompt_mask_identity(gpu):
 # of more than 128 tiles; the comment gives (KV parts, tiles per item, items per KV head).
 LONG_ITEMS = [
     (200, 32768, False),   # (2, 171, 32): the dense tail in pieces of 170-171 tiles
-    (512, 32768, False),   # (2, 147, 40): BASELINE-sized chunk, pieces of 146-147 tiles
-    (640, 32768, False),   # (2, 147, 44)
-    (2048, 24576, False),  # (2, 154, 80)
-    (384, 4200, True),     # (4, 132, 12): pieces of 129-132 tiles -- a few tiles into table block 2
+    (512, 40000, False),   # (2, 157, 44): BASELINE-sized chunk, pieces of 156-157 tiles
+    (1024, 65536, False),  # (2, 256, 60): pieces of exactly four table blocks
+    (512, 4200, True),     # (4, 132, 16): pieces of 129-132 tiles -- a few tiles into table block 2
     (200, 9000, True),     # (4, 141, 14)
     (96, 24576, True),     # (4, 154, 15)
     (96, 32768, True),     # (4, 205, 15)
@@ -150,6 +149,8 @@ LONG_ITEMS = [
     (512, 20000, True),    # (2, 313, 32)
     (512, 24576, True),    # (2, 384, 32): six table blocks
     (256, 32768, True),    # (2, 256, 32)
+    (640, 16384, True),    # (1, 171, 60): KV whole, rows of 493-512 tiles in three pieces
+    (2048, 12345, True),   # (1, 386, 64): KV whole, rows of 323-386 tiles unsplit
 ]
 
 

@@ -1,7 +1,7 @@
 """Long-context correctness: BASELINE config 4 (L = 32768 and 131072, chunk 2048).
 
 At L = 131072 a dense-tail row attends 131072 keys = 4096 tiles: the
-TriangleMix op splits those rows over the GPU (eight pieces of 512 tiles,
+TriangleMix op splits those rows over the GPU (sixteen pieces of 256 tiles,
 merged inside the launch) and the dense companion runs each of its 64 row
 blocks as one item of ~4096 tiles; the position, row-index and page
 arithmetic run at sizes no other test reaches.  The reference pins its
@@ -14,7 +14,7 @@ fp32 oracle runs on the GPU in its blocked form, so whole chunks are checked.
   prompt's last chunk and of a middle chunk, for the TriangleMix op, and of
   the dense companion's last chunk; tolerances as everywhere (max-abs 2e-2,
   mean-abs 2e-3, rel-L2 2e-2), the mean also per 32-row block.
-* The exact mask identity over the WHOLE last chunk (KV halves) and a whole
+* The exact mask identity over the WHOLE last chunk (KV whole, dense-tail rows in pieces) and a whole
   middle chunk at L = 32768 (KV whole: four-wave workgroups, two per CU,
   one wave per head over every tile): Q = 0 weighs every
   attended key 1/|S|, and one-hot residue V rows turn each output row into
@@ -74,8 +74,9 @@ def test_long_context_rows_match_oracle(gpu, L):
         plan = cabi.chunk_plan(CHUNK, qs, seq, prompt)
         print(f"L={L} {label} chunk qs={qs} plan={plan} "
               f"workspace={cabi.workspace_size(CHUNK, qs, seq, prompt)}", flush=True)
-        # the middle chunk runs as KV whole (four-wave workgroups, two per CU), the last as KV halves
-        assert plan[0] == (1 if label == "middle" else 2), plan
+        # both run as KV whole (four-wave workgroups, two per CU); the last chunk cuts its dense-tail rows
+        # into pieces merged inside the launch
+        assert plan[0] == 1, plan
         got = _sparse(gpu, qd, kd, vd, btd, qs, seq, prompt)
         _check_all_rows(f"L={L} {label} rows {qs}..{seq - 1}", got, qd, kd, vd, btd, qs, seq, prompt)
     assert cabi.workspace_size(CHUNK, L - CHUNK, L, prompt) > cabi.WORKSPACE_COUNTER_BYTES  # dense tail split
@@ -111,7 +112,7 @@ def _residue_histogram(intervals, m):
 
 @pytest.mark.parametrize("L,where", [(32768, "last"), (131072, "last"), (32768, "middle")])
 def test_long_context_mask_identity_whole_chunk(gpu, L, where):
-    """Every row of a 2048-row chunk: the last one (KV halves, dense-tail rows split over KV) and a middle
+    """Every row of a 2048-row chunk: the last one (KV whole, dense-tail rows split over KV) and a middle
     one (KV whole)."""
     qs = L - CHUNK if where == "last" else L // 2
     seq, prompt = qs + CHUNK, L
