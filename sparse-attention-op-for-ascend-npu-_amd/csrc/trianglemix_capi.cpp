@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <vector>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 
 #include "../../include/trianglemix.h"
@@ -233,7 +234,10 @@ struct ChunkPlan {
 };
 
 // The best (shape, T) among the shapes' candidates, in the order given
-// (earlier shapes and larger T win ties); nullopt-like {0, 0} when none fits.
+// (earlier shapes and larger T win ties).  Each shape's candidates include a
+// plan that splits nothing (T at or above the longest row), which always fits
+// the workspace bound; should no candidate fit, the first shape runs every
+// row unsplit.
 struct ShapeCandidates {
   int kv_parts;
   const PlanModel* model;
@@ -261,6 +265,7 @@ ChunkPlan best_plan(const std::vector<int>& row_tiles, std::initializer_list<Sha
       }
     }
   }
+  if (best.kv_parts == 0) best = {shapes.begin()->kv_parts, std::max(longest, 1)};
   return best;
 }
 
