@@ -18,6 +18,7 @@
 #include <vector>
 #include <cstring>
 #include <initializer_list>
+#include <limits>
 #include <mutex>
 
 #include "../../include/trianglemix.h"
@@ -177,8 +178,11 @@ bool layout_fits(const SplitLayout& s) {
   return s.split_row_blocks <= tmx::kMaxSplitRowBlocks && s.split_items <= tmx::kMaxSplitItems;
 }
 
-// The simulated time of a plan (see above): a min-heap of slot loads.
-double simulated_time(const std::vector<int>& row_tiles, int T, const PlanModel& m) {
+// The simulated time of a plan (see above): a min-heap of slot loads.  Slot
+// loads and merge completions only grow, so the simulation stops, returning
+// a time above `limit`, as soon as either exceeds it: such a plan cannot beat
+// the best one so far.
+double simulated_time(const std::vector<int>& row_tiles, int T, const PlanModel& m, double limit) {
   double heap[kMaxSlots] = {};  // all zero: a valid min-heap
   auto add_to_least = [&](double cost) {
     const double v = heap[0] + cost;  // replace the root, sift down
@@ -206,6 +210,7 @@ double simulated_time(const std::vector<int>& row_tiles, int T, const PlanModel&
       last = std::max(last, add_to_least(cost));
     }
     if (pieces > 1) merged = std::max(merged, last + m.merge_fixed + m.merge_per_piece * pieces);
+    if (last > limit || merged > limit) return std::max(last, merged);
   }
   double end = merged;
   for (int k = 0; k < m.slots; ++k) end = std::max(end, heap[k]);
@@ -258,7 +263,8 @@ ChunkPlan best_plan(const std::vector<int>& row_tiles, std::initializer_list<Sha
         unsplit_done = true;
       }
       if (!layout_fits(split_layout(row_tiles, tk))) continue;
-      const double t = simulated_time(row_tiles, tk, *s.model);
+      const double t = simulated_time(row_tiles, tk, *s.model,
+                                      best.kv_parts == 0 ? std::numeric_limits<double>::infinity() : best_time);
       if (best.kv_parts == 0 || t < best_time) {
         best = {s.kv_parts, tk};
         best_time = t;
@@ -308,10 +314,10 @@ ChunkPlan choose_plan(const std::vector<int>& row_tiles, bool sparse) {
 }
 
 // The choice depends only on the chunk geometry, which repeats for every layer
-// of a step: a per-thread cache keeps the simulation (10-250 us on the host)
-// off the launch path.  64 entries hold every chunk of a 131072-token prefill
-// in chunks of 2048, so even a sequence of distinct chunks repeated layer by
-// layer plans each chunk once.
+// of a step: a per-thread cache keeps the simulation (4-200 us on the host for
+// a chunk, a few ms for a whole long prompt) off the launch path.  64 entries
+// hold every chunk of a 131072-token prefill in chunks of 2048, so even a
+// sequence of distinct chunks repeated layer by layer plans each chunk once.
 struct PlanKey {
   int64_t num_row_blocks, query_start, seq_len, sparse_begin, sparse_end;
   bool operator==(const PlanKey& o) const {
