@@ -92,10 +92,11 @@ int check_attributes(int64_t query_tokens, int64_t query_start, int64_t seq_len,
 // passes, HIP events): 87 TriangleMix and dense-companion chunks of 64 to
 // 12288 rows at prompts of 1024 to 131072 tokens, 35 of them held out of the
 // first fit to check it.  The fit minimised the time the planned plans lose
-// to each geometry's fastest measured plan.  Summed over the 87 chunks the
-// planned plans lose 46 us of 6,479 us (0.7 %); charging the merge to the
-// whole chunk instead of the split rows, with the earlier costs and candidate
-// rules, lost 189 us.
+// to each geometry's fastest measured plan.  On the committed sweep
+// (tests/plan_sweep_mi355x.json) the planned plans lose 43.5 us of the
+// 6,533 us the 87 chunks take at their fastest (0.67 %); the previous
+// planner, which charged the merge to the whole chunk instead of the split
+// rows and never split KV-whole items, lost 212 us (3.2 %).
 //  * TriangleMix chunks of up to 16 row blocks: quarters (T from the ladder,
 //    32-128 tiles) or halves (T of 24 tiles and more).  Quarters stay on the
 //    ladder: their longer items move twice the K/V of halves ones per head.
