@@ -18,6 +18,8 @@ Reported JSON line (rank 0 only):
   (4*D*Hq*attended pairs) / average launch duration, vs 2.5 PFLOP/s;
   ``traffic`` is the rocprofv3 FETCH+WRITE bytes per launch when a summary
   for this workload exists under profiles/, else null;
+* ``plans`` -- each chunk's launch plan: [KV parts, tiles per work item, work
+  items per KV head];
 * ``dense`` -- the same 16 chunks through the dense paged causal companion
   kernel, and the attention-time cut of sparse vs dense;
 * ``library_dense`` -- the same 16 chunks through PyTorch's own dense
@@ -176,6 +178,14 @@ def abba(run_a, run_b, steps: int, windows: int):
     return out["a"][0], out["a"][1], out["b"][0], out["b"][1]
 
 
+def chunk_plans(chunks) -> list[list[int]]:
+    """Per chunk, the TriangleMix launch plan the library takes: [KV parts, tiles per work item, work items per
+    KV head] (4 / 2 / 1 = KV quarters / halves / whole)."""
+    from trianglemix import cabi
+
+    return [list(cabi.chunk_plan(c.query_tokens, c.query_start, c.seq_len, c.prompt_len)) for c in chunks]
+
+
 def chunk_set_line(args, headline: bool) -> dict:
     """The JSON line of one chunk set (config 2 by default; config 1 or 3 with --workload)."""
     import torch
@@ -262,6 +272,7 @@ def chunk_set_line(args, headline: bool) -> dict:
             "kv_hbm_gbs": round(kvb / (ms_sparse * 1e-3) / 1e9, 1),
         },
         "per_chunk_us": m["per_chunk_us"],
+        "plans": chunk_plans(chunks),
         "dense": {
             "ms_per_step": round(ms_dense, 5),
             "us_per_chunk": round(ms_dense * 1000.0 / n, 3),
@@ -389,6 +400,7 @@ def headline_legs(args) -> dict:
         flops = sum(chunk_flops(c) for c in chunks)
         leg = {"us_per_chunk": round(m["ms_sparse"] * 1000.0 / n, 3),
                "per_chunk_us": m["per_chunk_us"],
+               "plans": chunk_plans(chunks),
                "mfma_frac": round(flops / (m["ms_sparse"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                "executed_tile_frac": round(sum(executed_flops(c) for c in chunks) / (m["ms_sparse"] * 1e-3) / 1e12
                                            / PEAK_BF16_TFLOPS, 4),
