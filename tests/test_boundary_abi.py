@@ -467,7 +467,7 @@ def _items_at(T: int, qs: int, tq: int, seq: int, prompt: int | None) -> tuple[i
 def test_long_chunk_plan_skips_the_simulation_and_takes_the_largest_items(lib):
     """A chunk with more than 4096 candidate items (total tiles / 32, the smallest split) is not simulated:
     its tiles spread over one item per slot -- T is the smallest candidate of at least total / slots tiles
-    (csrc/trianglemix_capi.cpp choose_tiles_per_split), which for such a chunk is the longest row: no split.
+    (csrc/trianglemix_capi.cpp choose_plan), which for such a chunk is the longest row: no split.
     Pinned for the dense companion's last 2048-row chunk of a 131072-token prompt (64 row blocks of
     4033-4096 tiles): 64 items of whole rows, no workspace (2048 items and 1.1 GB of partials when an item
     held at most 128 tiles).  The TriangleMix chunk at the same place has 17458 tiles (sparse rows of 18
