@@ -81,10 +81,13 @@ void simulate(int nplans, const int* sh, const int* rb0, const int* rb1, const i
 
 
 def _sim_lib():
-    d = Path(tempfile.mkdtemp(prefix="plan_fit_"))
-    (d / "sim.c").write_text(_SIM_C)
-    subprocess.run(["gcc", "-O2", "-shared", "-fPIC", str(d / "sim.c"), "-o", str(d / "sim.so")], check=True)
-    return ctypes.CDLL(str(d / "sim.so"))
+    """The simulation built from _SIM_C into a temporary directory, loaded, and the directory removed (the
+    loaded library stays mapped)."""
+    with tempfile.TemporaryDirectory(prefix="plan_fit_") as tmp:
+        d = Path(tmp)
+        (d / "sim.c").write_text(_SIM_C)
+        subprocess.run(["gcc", "-O2", "-shared", "-fPIC", str(d / "sim.c"), "-o", str(d / "sim.so")], check=True)
+        return ctypes.CDLL(str(d / "sim.so"))
 
 
 def source_costs() -> dict[str, list[float]]:
